@@ -1,0 +1,21 @@
+"""MI355X-native multi-scale deformable attention (MSDA).
+
+A drop-in for deformops' MSDA operator on AMD Instinct MI355X (gfx950): the
+``registry.msda`` call and the ``torch.ops.deformops.msda`` / ``msda_softmax``
+operators, backed by hand-written HIP kernels (forward, and a backward that
+accumulates ``grad_value`` with atomics in place).
+"""
+
+from __future__ import annotations
+
+from .version import __version__
+
+__all__ = ["__version__", "registry"]
+
+
+def __getattr__(name: str):
+    if name in ("registry", "core"):
+        import importlib  # noqa: PLC0415
+
+        return importlib.import_module(f".{name}", __name__)
+    raise AttributeError(name)

@@ -1,0 +1,141 @@
+/*
+ * deformops_amd: C ABI of the MI355X (gfx950) multi-scale deformable attention
+ * (MSDA) library, libdeformops_amd.so.
+ *
+ * Every pointer is a device pointer on the current HIP device, every buffer is
+ * owned by the caller, tensors are dense row-major (C-contiguous), and every call
+ * is stream-ordered on `stream` (a hipStream_t; NULL is the legacy default stream).
+ * The library never allocates device memory and never synchronizes. A call returns
+ * MSDA_OK or an error code; msda_last_error() then holds a message for the calling
+ * thread.
+ *
+ * Shape symbols: B batch, S = sum over levels of height * width, H heads, D
+ * channels per head, Q queries, L levels, P points per level.
+ *
+ *   value               [B, S, H, D]        value_dtype
+ *   spatial_shapes      [L, 2] (height, width) per level, index_dtype
+ *   level_start_index   [L]    exclusive prefix sum of height * width, index_dtype
+ *   sampling_locations  [B, Q, H, L, P, 2]  loc_dtype, normalized (x, y)
+ *   attention_weights   [B, Q, H, L * P]    value_dtype (raw logits when softmax != 0)
+ *   output              [B, Q, H * D]       value_dtype
+ *
+ * Sampling follows torch.nn.functional.grid_sample(mode="bilinear",
+ * padding_mode="zeros", align_corners=False): pixel = loc * size - 0.5, corners
+ * outside the level contribute zero, and a sample outside -1 <= pixel < size (or
+ * with a NaN coordinate) contributes nothing and has zero gradient.
+ */
+#ifndef DEFORMOPS_AMD_H_
+#define DEFORMOPS_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSDA_ABI_VERSION 1
+
+/* Element types. value and attention_weights share one; locations may be
+ * MSDA_F32 or the value type (MSDA_F64 only with MSDA_F64 values). */
+enum msda_dtype {
+  MSDA_F32 = 0,
+  MSDA_F16 = 1,
+  MSDA_BF16 = 2,
+  MSDA_F64 = 3,
+};
+
+/* Element types of spatial_shapes and level_start_index. */
+enum msda_index_dtype {
+  MSDA_I64 = 0,
+  MSDA_I32 = 1,
+};
+
+/* Bits of the flags argument. */
+enum msda_flags {
+  MSDA_SOFTMAX = 1,               /* normalize attention_weights over the L * P points */
+  MSDA_ACCUMULATE_GRAD_VALUE = 2, /* backward: add into grad_value instead of overwriting it */
+};
+
+/* Return codes. */
+enum msda_status {
+  MSDA_OK = 0,
+  MSDA_ERR_INVALID = 1,     /* a null pointer, a negative size or an unknown dtype */
+  MSDA_ERR_UNSUPPORTED = 2, /* a valid call this build has no kernel for */
+  MSDA_ERR_HIP = 3,         /* a HIP runtime error at launch */
+};
+
+/*
+ * Forward: output[b, q, h*D + d] = sum over (l, p) of
+ *   w[b,q,h,l,p] * bilinear(value[b, level l, :, h, d], loc[b,q,h,l,p]),
+ * with w = attention_weights, or their softmax over the L * P points of each
+ * (b, q, h) when flags has MSDA_SOFTMAX. The output is written in full (zeros when
+ * L * P == 0).
+ *
+ * Replaces the forward operator the reference binds through the torch
+ * dispatcher: deformops_cuda::msda_fp32acc[_softmax]_forward
+ * (sources/deformops/backends/cuda/_schema.py:18-23, boxed entry
+ * include/msda_boxed.cuh:14-28, host launch include/msda_launch.cuh:63-138).
+ */
+int msda_forward(const void* value, int value_dtype,
+                 const void* spatial_shapes, const void* level_start_index,
+                 int index_dtype,
+                 const void* sampling_locations, int loc_dtype,
+                 const void* attention_weights,
+                 void* output,
+                 int64_t batch, int64_t spatial, int64_t heads, int64_t channels,
+                 int64_t queries, int64_t levels, int64_t points,
+                 int flags, void* stream);
+
+/*
+ * Backward of msda_forward for the upstream gradient grad_output [B, Q, H * D]
+ * (value_dtype). Writes
+ *   grad_value               [B, S, H, D]        value_dtype
+ *   grad_sampling_locations  [B, Q, H, L, P, 2]  loc_dtype
+ *   grad_attention_weights   [B, Q, H, L * P]    value_dtype (w.r.t. the logits
+ *                                                 under MSDA_SOFTMAX)
+ * grad_value is zero-filled by this call (by a kernel, not hipMemsetAsync, so the
+ * call may be captured in a HIP graph) unless flags has MSDA_ACCUMULATE_GRAD_VALUE,
+ * and is then accumulated with device-scope atomics in its own dtype (packed bf16
+ * / f16 atomics for 16-bit values): no scratch buffer and no float32 copy. The
+ * summation order, and so the last bits of grad_value, vary between runs. The other
+ * two gradients are written in full, zeros included.
+ *
+ * Replaces deformops_cuda::msda_fp32acc[_softmax]_backward
+ * (sources/deformops/backends/cuda/_schema.py:24-29, include/msda_boxed.cuh:32-53,
+ * include/msda_launch.cuh:140-275), which needs float32 copies of every input and
+ * a float32 scratch grad_value for 16-bit inputs.
+ */
+int msda_backward(const void* value, int value_dtype,
+                  const void* spatial_shapes, const void* level_start_index,
+                  int index_dtype,
+                  const void* sampling_locations, int loc_dtype,
+                  const void* attention_weights,
+                  const void* grad_output,
+                  void* grad_value, void* grad_sampling_locations,
+                  void* grad_attention_weights,
+                  int64_t batch, int64_t spatial, int64_t heads, int64_t channels,
+                  int64_t queries, int64_t levels, int64_t points,
+                  int flags, void* stream);
+
+/* The message of the calling thread's last failed call ("" if none). Replaces the
+ * std::runtime_error text of TORCH_CHECK (include/stable_compat.cuh:33-46). */
+const char* msda_last_error(void);
+
+/* MSDA_ABI_VERSION of the loaded library. */
+int msda_abi_version(void);
+
+/* The launch layout msda_forward / msda_backward would use for these sizes:
+ * channels per lane, lanes per (query, head) unit and waves per workgroup. Host
+ * only; lets a caller or a test check the geometry without a GPU. Returns MSDA_OK
+ * or the error code the compute call would return. */
+int msda_launch_geometry(int value_dtype, int64_t batch, int64_t spatial,
+                         int64_t heads, int64_t channels, int64_t queries,
+                         int64_t levels, int64_t points, int backward,
+                         int* channels_per_lane, int* lanes_per_unit,
+                         int* waves_per_block, int64_t* num_blocks);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DEFORMOPS_AMD_H_ */

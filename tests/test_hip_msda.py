@@ -1,0 +1,372 @@
+"""Parity of the HIP MSDA kernels with the CPU oracle, through the drop-in surface.
+
+Each test draws seeded inputs, runs ``deformops_amd.registry.msda`` (forward and
+autograd backward) on the GPU, and compares with the float64 C oracle on the same
+(rounded) inputs, norm-wise: ``max|actual - expected| / max|expected|`` (the form
+of the reference's tests/deformops/test_msda_shared_reduction_gpu.py:75-77).
+Tolerances: float32 forward 1e-5, float32 backward 1e-4
+(atomic summation order varies), bfloat16 / float16 2e-2 of the float64 result on
+the rounded inputs; float64 1e-10.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import oracle
+from deformops_amd.core.errors import NoBackendError
+from deformops_amd.registry import Backend, msda
+from oracle.eager import eager_msda
+from oracle.grid_sample_ref import grid_sample_msda
+from tests.workloads import CONFIGS, make_workload
+
+pytestmark = pytest.mark.gpu
+
+F32, BF16, F16, F64 = torch.float32, torch.bfloat16, torch.float16, torch.float64
+
+FWD_TOL = {F32: 1e-5, F64: 1e-10, BF16: 2e-2, F16: 2e-2}
+BWD_TOL = {F32: 1e-4, F64: 1e-10, BF16: 2e-2, F16: 2e-2}
+
+
+def rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    actual = actual.detach().to("cpu", torch.float64).reshape(expected.shape)
+    scale = expected.abs().max().item()
+    diff = (actual - expected).abs().max().item()
+    if scale == 0.0:
+        return diff
+    return diff / scale
+
+
+def run_hip(value, shapes, starts, loc, attn, grad_output, *, softmax, backend=None):
+    leaves = [t.detach().clone().requires_grad_(True) for t in (value, loc, attn)]
+    out = msda(
+        leaves[0], shapes, starts, leaves[1], leaves[2],
+        method="softmax" if softmax else "linear", backend=backend,
+    )
+    out.backward(grad_output)
+    torch.cuda.synchronize()
+    return out.detach(), leaves[0].grad, leaves[1].grad, leaves[2].grad
+
+
+def check_against_oracle(value, shapes, starts, loc, attn, grad_output, *, softmax, dtype, label=""):
+    out, gv, gl, ga = run_hip(value, shapes, starts, loc, attn, grad_output, softmax=softmax)
+    assert out.dtype == value.dtype and out.shape == (value.shape[0], loc.shape[1], value.shape[2] * value.shape[3])
+    assert gv.dtype == value.dtype and gl.dtype == loc.dtype and ga.dtype == attn.dtype
+    ref = oracle.forward(value, shapes, starts, loc, attn, softmax=softmax)
+    rgv, rgl, rga = oracle.backward(value, shapes, starts, loc, attn, grad_output, softmax=softmax)
+    errs = {
+        "output": rel_err(out, ref),
+        "grad_value": rel_err(gv, rgv),
+        "grad_loc": rel_err(gl, rgl),
+        "grad_attn": rel_err(ga, rga.reshape(ga.shape)),
+    }
+    tols = {"output": FWD_TOL[dtype], "grad_value": BWD_TOL[dtype], "grad_loc": BWD_TOL[dtype],
+            "grad_attn": BWD_TOL[dtype]}
+    bad = {k: v for k, v in errs.items() if not v <= tols[k]}
+    assert not bad, f"{label} softmax={softmax}: relative errors {errs} exceed {tols}"
+    return errs
+
+
+# BASELINE configurations 0-3 at full size (config 4 has its own test below).
+CASES = [
+    pytest.param(0, F32, F32, id="cfg0-f32"),
+    pytest.param(1, F32, F32, id="cfg1-f32"),
+    pytest.param(2, BF16, BF16, id="cfg2-bf16"),
+    pytest.param(2, BF16, F32, id="cfg2-bf16-f32loc"),
+    pytest.param(2, F16, F16, id="cfg2-f16"),
+    pytest.param(3, F32, F32, id="cfg3-f32"),
+    pytest.param(3, BF16, BF16, id="cfg3-bf16"),
+]
+
+
+@pytest.mark.parametrize("softmax", [False, True], ids=["linear", "softmax"])
+@pytest.mark.parametrize(("cfg", "dtype", "loc_dtype"), CASES)
+def test_baseline_configs_match_oracle(device, cfg, dtype, loc_dtype, softmax):
+    w = make_workload(cfg).to(device, dtype, loc_dtype)
+    check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                         label=f"config {cfg}")
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize(("dtype", "loc_dtype"), [(BF16, BF16), (F16, F16), (BF16, F32)],
+                         ids=["bf16", "f16", "bf16-f32loc"])
+def test_headline_config_full_size_matches_oracle(device, dtype, loc_dtype):
+    """Config 4 (B=4, Q=S=21,504, bf16) at full size, both methods."""
+    w = make_workload(4).to(device, dtype, loc_dtype)
+    for softmax in (False, True):
+        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                             label="config 4")
+
+
+def test_headline_config_float32(device):
+    w = make_workload(4, batch=1).to(device, F32)
+    check_against_oracle(*w.operands(), w.grad_output, softmax=False, dtype=F32, label="config 4 f32")
+
+
+# Shape coverage beyond the BASELINE configurations.
+
+SHAPES = [
+    # (levels, B, Q, H, D, P)
+    pytest.param(((8, 8),), 1, 5, 1, 16, 4, id="one-level"),
+    pytest.param(((8, 8), (4, 4), (2, 2)), 2, 12, 4, 32, 4, id="three-levels"),
+    pytest.param(((7, 5), (3, 3)), 1, 9, 8, 16, 8, id="eight-points"),
+    pytest.param(((1, 1),), 3, 4, 2, 16, 1, id="1x1-level"),
+    pytest.param(((6, 9), (3, 5)), 2, 7, 3, 24, 3, id="odd-heads-d24-p3"),
+    pytest.param(((6, 6), (3, 3)), 1, 10, 2, 8, 2, id="d8"),
+    pytest.param(((9, 7), (5, 4)), 2, 33, 4, 64, 4, id="d64"),
+    pytest.param(((9, 7),), 1, 17, 2, 128, 4, id="d128"),
+    pytest.param(((5, 5),), 1, 6, 2, 7, 2, id="d7"),
+    pytest.param(((10, 12), (5, 6), (3, 3), (2, 2), (1, 1)), 2, 21, 8, 32, 4, id="five-levels"),
+    pytest.param(((12, 10), (6, 5)), 1, 13, 1, 256, 2, id="d256"),
+]
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16, F64], ids=["f32", "bf16", "f16", "f64"])
+@pytest.mark.parametrize(("levels", "B", "Q", "H", "D", "P"), SHAPES)
+def test_shapes_match_oracle(device, levels, B, Q, H, D, P, dtype):
+    if dtype == F64 and D // 2 > 64:
+        pytest.skip("float64 takes at most 64 lanes of 2 channels (D <= 128)")
+    w = make_workload(0, levels=levels, batch=B, queries=Q, heads=H, channels=D, points=P, seed=Q + D)
+    w = w.to(device, dtype)
+    for softmax in (False, True):
+        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                             label=f"levels={levels} B={B} Q={Q} H={H} D={D} P={P}")
+
+
+# Boundary semantics.
+
+
+def test_pixel_boundary_table_matches_grid_sample(device):
+    """Exact pixel transitions (reference tests/deformops/test_msda_eager.py:54-80)."""
+    W = H = 4
+    shapes = torch.tensor([[H, W]], device=device)
+    starts = torch.tensor([0], device=device)
+    value = torch.arange(H * W, dtype=F32, device=device).view(1, H * W, 1, 1)
+    coords = [0.0, 0.125, 0.375, 0.5, 1.0, -0.125, 1.25]
+    pts = [(cx, cy) for cx in coords for cy in coords]
+    loc = torch.tensor(pts, dtype=F32, device=device).view(1, 1, 1, 1, len(pts), 2)
+    attn = torch.ones(1, 1, 1, len(pts), dtype=F32, device=device)
+    # One point per call, so each sample's value is visible on its own.
+    for i in range(len(pts)):
+        out = msda(value, shapes, starts, loc[..., i : i + 1, :], attn[..., i : i + 1])
+        ref = grid_sample_msda(value.cpu(), shapes.cpu(), loc[..., i : i + 1, :].cpu(), attn[..., i : i + 1].cpu())
+        torch.testing.assert_close(out.cpu(), ref, atol=1e-6, rtol=1e-6, msg=f"point {pts[i]}")
+
+
+@pytest.mark.parametrize("softmax", [False, True], ids=["linear", "softmax"])
+def test_grid_aligned_locations_match_eager_gradients(device, softmax):
+    """Samples on integer pixels, -1 and the far edge included: one-sided gradients as
+    eager autograd gives them (reference tests/deformops/test_release_regressions.py:264-339)."""
+    g = torch.Generator().manual_seed(5)
+    levels = ((8, 8), (4, 4), (2, 2))
+    shapes = torch.tensor(levels)
+    areas = shapes.prod(1)
+    starts = torch.cat([areas.new_zeros(1), areas.cumsum(0)[:-1]])
+    B, Q, H, D, P = 2, 11, 4, 8, 4
+    value = torch.randn(B, int(areas.sum()), H, D, generator=g)
+    pixels = torch.randint(-2, 10, (B, Q, H, len(levels), P, 2), generator=g).float()
+    loc = (pixels + 0.5) / shapes.flip(1).view(1, 1, 1, -1, 1, 2)
+    attn = torch.randn(B, Q, H, len(levels) * P, generator=g)
+    grad = torch.linspace(-1, 1, B * Q * H * D).view(B, Q, H * D)
+
+    leaves = [t.clone().requires_grad_(True) for t in (value, loc, attn)]
+    expected = eager_msda(leaves[0], shapes, starts, leaves[1], leaves[2], softmax=softmax)
+    expected.backward(grad)
+    out, gv, gl, ga = run_hip(value.to(device), shapes.to(device), starts.to(device), loc.to(device),
+                              attn.to(device), grad.to(device), softmax=softmax)
+    for name, actual, ref in (("output", out, expected.detach()), ("value", gv, leaves[0].grad),
+                              ("location", gl, leaves[1].grad), ("attention", ga, leaves[2].grad)):
+        torch.testing.assert_close(actual.cpu(), ref, rtol=1e-4, atol=1e-5, msg=f"{name} differs")
+
+
+def test_all_out_of_bounds_is_zero(device):
+    w = make_workload(0, levels=((4, 4),), batch=1, queries=6, heads=2, channels=16).to(device, F32)
+    loc = torch.full_like(w.sampling_locations, 5.0)
+    out, gv, gl, ga = run_hip(w.value, w.spatial_shapes, w.level_start_index, loc, w.attention_weights,
+                              w.grad_output, softmax=False)
+    for t in (out, gv, gl, ga):
+        assert torch.count_nonzero(t) == 0
+
+
+@pytest.mark.parametrize("bad", [math.inf, -math.inf, math.nan])
+def test_nonfinite_locations_contribute_nothing(device, bad):
+    """A non-finite location is skipped: finite output and grad_value everywhere, the
+    other queries unchanged (reference tests/deformops/test_msda_backward_robustness.py)."""
+    w = make_workload(0, levels=((8, 8), (4, 4)), batch=2, queries=9, heads=2, channels=16).to(device, F32)
+    loc = w.sampling_locations.clone()
+    loc[:, 3] = bad
+    out, gv, gl, ga = run_hip(w.value, w.spatial_shapes, w.level_start_index, loc, w.attention_weights,
+                              w.grad_output, softmax=False)
+    assert torch.isfinite(out).all() and torch.isfinite(gv).all()
+    assert torch.count_nonzero(out[:, 3]) == 0
+    keep = [q for q in range(loc.shape[1]) if q != 3]
+    ref = oracle.forward(w.value, w.spatial_shapes, w.level_start_index, loc, w.attention_weights)
+    assert rel_err(out[:, keep], ref[:, keep]) <= 1e-5
+    rgv, rgl, _ = oracle.backward(w.value, w.spatial_shapes, w.level_start_index, loc, w.attention_weights,
+                                  w.grad_output)
+    assert rel_err(gv, rgv) <= 1e-4
+    assert rel_err(gl[:, keep], rgl[:, keep]) <= 1e-4
+
+
+def test_softmax_with_negative_infinite_logit(device):
+    """A -inf logit gets zero weight; the rest of the softmax is unaffected."""
+    w = make_workload(0, levels=((8, 8), (4, 4)), batch=1, queries=5, heads=2, channels=16).to(device, F32)
+    logits = w.logits.clone()
+    logits[..., 0] = -math.inf
+    out, *_ = run_hip(w.value, w.spatial_shapes, w.level_start_index, w.sampling_locations, logits,
+                      w.grad_output, softmax=True)
+    ref = oracle.forward(w.value, w.spatial_shapes, w.level_start_index, w.sampling_locations, logits,
+                         softmax=True)
+    assert rel_err(out, ref) <= 1e-5
+
+
+# Operand handling.
+
+
+@pytest.mark.parametrize("axis", ["batch", "queries"])
+def test_empty_calls(device, axis):
+    sizes = {"batch": 0} if axis == "batch" else {"queries": 0}
+    w = make_workload(0, levels=((4, 4),), heads=2, channels=16, **{"batch": 1, "queries": 3, **sizes})
+    w = w.to(device, F32)
+    out, gv, gl, ga = run_hip(w.value, w.spatial_shapes, w.level_start_index, w.sampling_locations,
+                              w.attention_weights, w.grad_output, softmax=False)
+    assert out.shape == (w.value.shape[0], w.sampling_locations.shape[1], 32)
+    assert gv.shape == w.value.shape and torch.count_nonzero(gv) == 0
+
+
+@pytest.mark.parametrize("method", ["linear", "softmax"])
+def test_non_contiguous_operands(device, method):
+    """Views with odd strides give the contiguous result and route gradients to the
+    leaves (reference tests/deformops/test_release_regressions.py:154-214)."""
+    w = make_workload(0, levels=((8, 8), (4, 4)), batch=2, queries=10, heads=2, channels=16).to(device, F32)
+    value_leaf = w.value.transpose(1, 2).contiguous().requires_grad_(True)
+    packed = torch.cat([w.sampling_locations, torch.rand_like(w.sampling_locations)], -1).requires_grad_(True)
+    weights = w.logits if method == "softmax" else w.attention_weights
+    attn_packed = torch.cat([weights, torch.rand_like(weights)], -1).requires_grad_(True)
+    out = msda(value_leaf.transpose(1, 2), w.spatial_shapes, w.level_start_index, packed[..., :2],
+               attn_packed[..., : weights.shape[-1]], method=method)
+    out.backward(w.grad_output)
+    ref_out, gv, gl, ga = run_hip(w.value, w.spatial_shapes, w.level_start_index, w.sampling_locations,
+                                  weights, w.grad_output, softmax=method == "softmax")
+    close = {"rtol": 1e-5, "atol": 1e-6}
+    torch.testing.assert_close(out.detach(), ref_out, **close)
+    torch.testing.assert_close(value_leaf.grad.transpose(1, 2), gv, **close)
+    torch.testing.assert_close(packed.grad[..., :2], gl, **close)
+    assert torch.count_nonzero(packed.grad[..., 2:]) == 0
+    torch.testing.assert_close(attn_packed.grad[..., : weights.shape[-1]], ga, **close)
+    assert torch.count_nonzero(attn_packed.grad[..., weights.shape[-1] :]) == 0
+
+
+def test_split_weights_and_int32_tables(device):
+    w = make_workload(0, levels=((8, 8), (4, 4)), batch=2, queries=7, heads=4, channels=32).to(device, F32)
+    B, S, H, D, Q, L, P = w.sizes
+    flat, *_ = run_hip(w.value, w.spatial_shapes, w.level_start_index, w.sampling_locations,
+                       w.attention_weights, w.grad_output, softmax=True)
+    split_w = w.attention_weights.view(B, Q, H, L, P)
+    split, _, _, ga = run_hip(w.value, w.spatial_shapes.int(), w.level_start_index.int(),
+                              w.sampling_locations, split_w, w.grad_output, softmax=True)
+    assert ga.shape == (B, Q, H, L, P)
+    torch.testing.assert_close(flat, split, rtol=0, atol=0)
+
+
+def test_softmax_equals_linear_on_normalized_weights(device):
+    """method="softmax" on logits equals "linear" on their softmax
+    (reference tests/deformops/test_msda_cpu_fallbacks.py:19-37)."""
+    w = make_workload(2, batch=1).to(device, F32)
+    a, *_ = run_hip(*w.operands(softmax=True), w.grad_output, softmax=True)
+    b, *_ = run_hip(w.value, w.spatial_shapes, w.level_start_index, w.sampling_locations,
+                    torch.softmax(w.logits, -1), w.grad_output, softmax=False)
+    torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("softmax", [False, True], ids=["linear", "softmax"])
+def test_float64_gradcheck(device, softmax):
+    """Finite-difference gradcheck in float64 (reference tests/deformops/test_msda_gradcheck.py)."""
+    w = make_workload(0, levels=((5, 6), (3, 2)), batch=1, queries=3, heads=2, channels=4, points=2,
+                      seed=11)
+    w = w.to(device, F64)
+    value, shapes, starts, loc, attn = w.operands(softmax=softmax)
+    # Keep samples away from pixel boundaries, where the location gradient is one-sided.
+    loc = (loc * 0.9 + 0.05).detach()
+
+    def fn(v, l, a):  # noqa: E741
+        return msda(v, shapes, starts, l, a, method="softmax" if softmax else "linear")
+
+    inputs = tuple(t.detach().clone().requires_grad_(True) for t in (value, loc, attn))
+    assert torch.autograd.gradcheck(fn, inputs, eps=1e-6, atol=1e-5, nondet_tol=1e-12)
+
+
+# Dispatch surface.
+
+
+def test_backend_selection_and_aliases(device):
+    w = make_workload(0, levels=((8, 8),), batch=1, queries=4, heads=2, channels=16).to(device, F32)
+    ops = w.operands()
+    auto = msda(*ops)
+    for backend in (Backend.HIP, Backend.CUDA):
+        torch.testing.assert_close(msda(*ops, backend=backend), auto, rtol=0, atol=0)
+    torch.testing.assert_close(torch.ops.deformops.msda(*ops), auto, rtol=0, atol=0)
+    torch.testing.assert_close(
+        torch.ops.deformops.msda_softmax(*w.operands(softmax=True)), msda(*w.operands(softmax=True), softmax=True)
+    )
+    with pytest.raises(NoBackendError):
+        msda(*ops, backend=Backend.TRITON)
+    with pytest.raises(NoBackendError, match="not part of this build"):
+        msda(*(t.cpu() for t in ops))
+
+
+def test_unsupported_head_dim_raises_no_backend_error(device):
+    w = make_workload(0, levels=((4, 4),), batch=1, queries=2, heads=1, channels=1030).to(device, F32)
+    with pytest.raises(NoBackendError, match="does not support"):
+        msda(*w.operands(), backend=Backend.HIP)
+
+
+def test_malformed_operands_raise_value_error(device):
+    w = make_workload(0, levels=((4, 4), (2, 2)), batch=1, queries=8, heads=2, channels=16).to(device, F32)
+    value, shapes, starts, loc, attn = w.operands()
+    for bad in (
+        (value, shapes, starts, torch.rand(*loc.shape[:-1], 3, device=device), attn),
+        (value, shapes, starts, loc, attn[..., :-1]),
+        (value, shapes, starts, loc, attn.half()),
+    ):
+        with pytest.raises(ValueError):  # noqa: PT011
+            msda(*bad, backend=Backend.HIP)
+
+
+def test_malformed_level_table_reads_nothing_out_of_bounds(device):
+    """A level table that overruns value samples nothing from the bad level."""
+    w = make_workload(0, levels=((8, 8), (4, 4)), batch=1, queries=6, heads=2, channels=16).to(device, F32)
+    bad_shapes = torch.tensor([[8, 8], [40, 40]], device=device)
+    out = msda(w.value, bad_shapes, w.level_start_index, w.sampling_locations, w.attention_weights)
+    keep = w.sampling_locations.clone()
+    ref_w = w.attention_weights.view(1, 6, 2, 2, 4).clone()
+    ref_w[:, :, :, 1] = 0
+    ref = oracle.forward(w.value, w.spatial_shapes, w.level_start_index, keep, ref_w.view(1, 6, 2, 8))
+    assert rel_err(out, ref) <= 1e-5
+
+
+# Precision of the native-dtype atomics.
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
+def test_grad_value_atomics_are_unbiased(device, dtype):
+    """|cos(mean error, fp64 gradient)| < 0.05 over 4 runs
+    (reference tests/deformops/test_msda_bias.py:23-109)."""
+    levels = ((48, 48), (24, 24), (12, 12))
+    w = make_workload(0, levels=levels, batch=2, queries=1024, heads=8, channels=32, seed=1958)
+    loc = w.sampling_locations * 0.8 + 0.1
+    ones = torch.ones_like(w.grad_output)
+    gt, _, _ = oracle.backward(w.value, w.spatial_shapes, w.level_start_index, loc, w.logits, ones,
+                               softmax=True, pixel_f32=False)
+    errors = []
+    for _ in range(4):
+        _, gv, _, _ = run_hip(w.value.to(device, dtype), w.spatial_shapes.to(device),
+                              w.level_start_index.to(device), loc.to(device, dtype), w.logits.to(device, dtype),
+                              ones.to(device, dtype), softmax=True)
+        errors.append(gv.double().cpu() - gt)
+    mean_err = torch.stack(errors).mean(0)
+    cos = (mean_err * gt).sum().item() / (mean_err.norm().item() * gt.norm().item() + 1e-30)
+    assert abs(cos) < 0.05, f"directional grad_value bias cos={cos:+.3f}"
