@@ -70,10 +70,11 @@ def time_fwd_bwd(w, steps: int, warmup: int, softmax: bool):
 
 
 def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
-    """Average device time of each kernel alone, through the C ABI, on torch's stream.
+    """Average device time of each direction alone, through the C ABI, on torch's stream.
 
-    The backward is launched with MSDA_ACCUMULATE_GRAD_VALUE after a zero-fill
-    outside the timed pair, so its events bracket the backward kernel only.
+    The forward is one kernel; the backward is one kernel for the linear method
+    (the owner-computes grad_value kernel, which also writes the location and
+    weight gradients), plus the softmax-Jacobian kernel for the softmax method.
     """
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
 
@@ -81,7 +82,7 @@ def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
     value, shapes, starts, loc, attn = w.operands(softmax=softmax)
     B, S, H, D, Q, L, P = w.sizes
     out = torch.empty((B, Q, H * D), dtype=value.dtype, device=value.device)
-    gv = torch.zeros_like(value)
+    gv = torch.empty_like(value)
     gl = torch.empty_like(loc)
     ga = torch.empty_like(attn)
     stream = torch.cuda.current_stream()
@@ -98,8 +99,7 @@ def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
         lib.check(lib.backward(value.data_ptr(), vcode, shapes.data_ptr(), starts.data_ptr(), icode,
                                loc.data_ptr(), lcode, attn.data_ptr(), w.grad_output.data_ptr(),
                                gv.data_ptr(), gl.data_ptr(), ga.data_ptr(),
-                               B, S, H, D, Q, L, P, flags | _lib.FLAG_ACCUMULATE_GRAD_VALUE,
-                               stream.cuda_stream))
+                               B, S, H, D, Q, L, P, flags, stream.cuda_stream))
 
     result = {}
     for name, fn in (("forward", fwd), ("backward", bwd)):
@@ -108,8 +108,6 @@ def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
         torch.cuda.synchronize()
         times = []
         for _ in range(steps):
-            if name == "backward":
-                gv.zero_()
             s, e = _events(2)
             s.record(stream)
             fn()
@@ -117,19 +115,6 @@ def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
             times.append((s, e))
         torch.cuda.synchronize()
         result[name] = statistics.mean(s.elapsed_time(e) for s, e in times)
-    # The zero-fill the default backward runs first, timed on its own.
-    fill_times = []
-    for _ in range(max(steps // 4, 5)):
-        s, e = _events(2)
-        s.record(stream)
-        lib.check(lib.backward(value.data_ptr(), vcode, shapes.data_ptr(), starts.data_ptr(), icode,
-                               loc.data_ptr(), lcode, attn.data_ptr(), w.grad_output.data_ptr(),
-                               gv.data_ptr(), gl.data_ptr(), ga.data_ptr(),
-                               B, S, H, D, 0, L, P, flags, stream.cuda_stream))
-        e.record(stream)
-        fill_times.append((s, e))
-    torch.cuda.synchronize()
-    result["grad_value_fill"] = statistics.mean(s.elapsed_time(e) for s, e in fill_times)
     return result
 
 
@@ -234,13 +219,12 @@ def main() -> int:
             "median_ms_per_step": round(median_ms, 5),
             "forward_kernel_ms": round(kernels["forward"], 5),
             "backward_kernel_ms": round(kernels["backward"], 5),
-            "grad_value_fill_ms": round(kernels["grad_value_fill"], 5),
             "forward_kernel_gb_s": round(fwd_bytes / (kernels["forward"] * 1e-3) / 1e9, 1),
             "device": torch.cuda.get_device_name(device),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "msda_backward_kernel",
+            "kernel": "msda_backward_owner_kernel",
             "achieved": round(bwd_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

@@ -27,7 +27,7 @@ ARCH = os.environ.get("DEFORMOPS_AMD_ARCH", "gfx950")
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
     "-shared",
     # Packed fp32 VALU ops stay off: hipcc forms them from ordinary float code.

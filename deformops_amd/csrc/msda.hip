@@ -39,6 +39,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -438,9 +439,389 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
 
 // ---------------------------------------------------------------------------
 // Backward.
+//
+// Three kernels on the caller's stream, no atomics to global memory and no buffer
+// beyond the three gradients:
+//
+//   msda_row_summary_kernel    For every (b, h, l) and block of QB queries (QB * P2
+//                              = 64 sample slots, P2 = P rounded up to a power of
+//                              two), the range of level-l rows its in-bounds
+//                              corners touch. Stored, as scratch, at the start of
+//                              grad_sampling_locations, which is always large enough
+//                              and is written for real only by the third kernel.
+//   msda_grad_value_kernel     Owner-computes grad_value: one 1024-thread workgroup
+//                              per chunk of NPOS positions of one (b, h) keeps the
+//                              chunk's gradient in LDS (fp32; fp64 for double).
+//                              Its 16 waves walk the query blocks of every level
+//                              that meets the chunk, skip blocks whose row range
+//                              misses it, and add a * w_c * grad_out[b, q, h, :] for
+//                              the corners inside the chunk with LDS atomics. The
+//                              chunk is then written once with plain stores: every
+//                              element of grad_value has exactly one writer, so the
+//                              result needs no zero-fill, accumulates in fp32 and
+//                              does not depend on scheduling beyond fp32 rounding.
+//   msda_grad_sample_kernel    Sample-parallel, laid out like the forward: gathers
+//                              the four corners of each sample, forms
+//                              G_c = <grad_out, value_c>, reduces it across the
+//                              unit's lanes and writes grad_loc and grad_attn (the
+//                              softmax Jacobian included). Runs last, so it
+//                              overwrites the row summaries.
 
+// grad_value, owner-computes, with the chunk accumulator in registers.
+//
+// Workgroup (b, h, chunk) owns NPOS consecutive positions of grad_value[b, :, h, :].
+// Thread t owns the "items" t, t + T, t + 2T, t + 3T (T threads): item i is position
+// i / G and channel group i % G (G = D / CVR groups of CVR channels), so the whole
+// chunk lives in fp32 (fp64) registers. Per batch of up to one query block per
+// wave:
+//   A. each wave stages its block's grad_out vectors in LDS and turns every sample
+//      of the block into up to four corner records (position in the chunk, query
+//      slot, attention * bilinear weight) kept in registers;
+//   B. a histogram of the records per position (LDS integer atomics);
+//   C. an exclusive scan of the histogram (the start of each position's run);
+//   D. each record claims a slot in its position's run (integer atomic) and is
+//      stored there;
+//   E. each thread walks the runs of the positions it owns and accumulates
+//      weight * grad_out into its registers with plain FMAs.
+// No floating-point atomics are used: on gfx950 the LDS ones retire at a fraction
+// of a lane per clock, while integer LDS atomics run near LDS store rate. Query
+// blocks whose row range misses the chunk are never loaded.
+
+constexpr int kGradValueMaxThreads = 1024;
+constexpr int kItemsPerThread = 4;
+constexpr int kRecordsPerWave = 4 * kWave;
+
+struct GradValuePlan {
+  int npos;       // positions per chunk
+  int nchunks;    // chunks per (b, h)
+  int p2_log2;    // log2 of P rounded up to a power of two
+  int nblocks;    // query blocks per (b, h, l): ceil(Q / QB), QB = 64 >> p2_log2
+  int groups;     // channel groups per position, G = D / CVR
+};
+
+struct alignas(8) RowRange {
+  int lo, hi;
+};
+
+template <typename A> struct alignas(8) SortedRec {
+  A w;
+  uint32_t qslot;  // wave * QB + query in block
+};
+
+// The normalized weight of sample s of a unit: the raw weight, or its softmax over
+// the unit's L * P logits (max first, so -inf logits are safe).
+template <typename T, bool SOFTMAX>
+__device__ inline typename Elem<T>::acc unit_weight(const T* unit_attn, int LP, int s) {
+  using A = typename Elem<T>::acc;
+  if constexpr (!SOFTMAX) {
+    return load_acc(unit_attn + s);
+  } else {
+    A mx = -INFINITY;
+    for (int i = 0; i < LP; ++i) mx = fmax(mx, load_acc(unit_attn + i));
+    A sum(0);
+    for (int i = 0; i < LP; ++i) sum += exp_acc(load_acc(unit_attn + i) - mx);
+    return exp_acc(load_acc(unit_attn + s) - mx) / sum;
+  }
+}
+
+// Inclusive prefix sum of v over the wave.
+__device__ inline int wave_inclusive_scan(int v) {
+  const int lane = threadIdx.x & (kWave - 1);
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int y = __shfl_up(v, d, kWave);
+    if (lane >= d) v += y;
+  }
+  return v;
+}
+
+// Exclusive prefix sum of one value per thread over the workgroup; *total gets the
+// sum. `wave_sums` holds one int per wave. Contains two barriers.
+__device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const int nwaves = int(blockDim.x) / kWave;
+  const int inc = wave_inclusive_scan(v);
+  if (lane == kWave - 1) wave_sums[wave] = inc;
+  __syncthreads();
+  int before = 0, all = 0;
+  for (int w = 0; w < nwaves; ++w) {
+    const int ws = wave_sums[w];
+    before += w < wave ? ws : 0;
+    all += ws;
+  }
+  __syncthreads();
+  *total = all;
+  return before + inc - v;
+}
+
+// The sample of lane `lane` in block j: (query, point), and whether it exists.
+struct BlockSlot {
+  int q, pt;
+  bool ok;
+};
+__device__ inline BlockSlot block_slot(const Problem& p, int p2_log2, int j, int lane) {
+  BlockSlot bs;
+  bs.q = (j << (6 - p2_log2)) + (lane >> p2_log2);
+  bs.pt = lane & ((1 << p2_log2) - 1);
+  bs.ok = bs.q < p.Q && bs.pt < p.P;
+  return bs;
+}
+
+// One wave per (b, h, l, block): the range of level-l rows the block's in-bounds
+// corners touch (lo > hi when none). Same geometry code and precision as the
+// grad_value kernel, so both place every corner in the same row.
+template <typename T, typename TL>
+__global__ __launch_bounds__(256) void msda_row_summary_kernel(const Problem p, const GradValuePlan gp,
+                                                               RowRange* __restrict__ out) {
+  using A = typename Elem<T>::acc;
+  const int64_t entries = int64_t(p.B) * p.H * p.L * gp.nblocks;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t e = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
+  if (e >= entries) return;  // uniform per wave
+  const int j = int(e % gp.nblocks);
+  const int l = int((e / gp.nblocks) % p.L);
+  const int h = int((e / (int64_t(gp.nblocks) * p.L)) % p.H);
+  const int b = int(e / (int64_t(gp.nblocks) * p.L * p.H));
+  int64_t hh, ww, st;
+  if (p.index_i32) {
+    hh = static_cast<const int32_t*>(p.shapes)[2 * l];
+    ww = static_cast<const int32_t*>(p.shapes)[2 * l + 1];
+    st = static_cast<const int32_t*>(p.starts)[l];
+  } else {
+    hh = static_cast<const int64_t*>(p.shapes)[2 * l];
+    ww = static_cast<const int64_t*>(p.shapes)[2 * l + 1];
+    st = static_cast<const int64_t*>(p.starts)[l];
+  }
+  const bool ok = hh > 0 && ww > 0 && st >= 0 && hh <= p.S && ww <= p.S && st + hh * ww <= p.S;
+  const Level lv = ok ? Level{int(hh), int(ww), int(st), 1} : Level{1, 1, 0, 0};
+  const BlockSlot bs = block_slot(p, gp.p2_log2, j, lane);
+  int lo = INT32_MAX, hi = INT32_MIN;
+  if (bs.ok) {
+    const int LP = p.L * p.P;
+    const int64_t unit = (int64_t(b) * p.Q + bs.q) * p.H + h;
+    const TL* lc = reinterpret_cast<const TL*>(p.loc) + (unit * LP + l * p.P + bs.pt) * 2;
+    const Geom<A> g = geometry<A>(load_acc(lc), load_acc(lc + 1), lv, 0u, 1u);
+    if (g.m00 || g.m01) lo = hi = (int(g.off[g.m00 ? 0 : 1]) - lv.start) / lv.w;
+    if (g.m10 || g.m11) {
+      const int r = (int(g.off[g.m10 ? 2 : 3]) - lv.start) / lv.w;
+      lo = min(lo, r);
+      hi = max(hi, r);
+    }
+  }
+  for (int m = 1; m < kWave; m <<= 1) {
+    lo = min(lo, __shfl_xor(lo, m, kWave));
+    hi = max(hi, __shfl_xor(hi, m, kWave));
+  }
+  if (lane == 0) out[e] = RowRange{lo, hi};
+}
+
+template <typename T, typename TL, int CVR, bool SOFTMAX>
+__global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
+    const Problem p, const GradValuePlan gp, const RowRange* __restrict__ rows, const int accumulate) {
+  using A = typename Elem<T>::acc;
+  constexpr int ES = Elem<T>::size;
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int nthreads = int(blockDim.x), nwaves = nthreads / kWave;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const int qb = kWave >> gp.p2_log2;
+  const int npos = gp.npos;
+
+  // LDS layout; every offset is an integer added to smem, so accesses stay ds_*.
+  size_t at = 0;
+  Level* levels = reinterpret_cast<Level*>(smem + at);
+  at += sizeof(Level) * size_t(p.L);
+  SortedRec<A>* sorted = reinterpret_cast<SortedRec<A>*>(smem + at);
+  at += sizeof(SortedRec<A>) * size_t(nwaves) * kRecordsPerWave;
+  T* gtile = reinterpret_cast<T*>(smem + at);
+  at += (sizeof(T) * size_t(nwaves) * qb * p.D + 15) & ~size_t(15);
+  int* cnt = reinterpret_cast<int*>(smem + at);
+  at += sizeof(int) * size_t(npos);
+  int* start = reinterpret_cast<int*>(smem + at);  // npos + 1 entries
+  at += sizeof(int) * size_t(npos + 1);
+  int* cursor = reinterpret_cast<int*>(smem + at);
+  at += sizeof(int) * size_t(npos);
+  int* blist = reinterpret_cast<int*>(smem + at);  // selected blocks, one per thread
+  at += sizeof(int) * size_t(nthreads);
+  int* wave_sums = reinterpret_cast<int*>(smem + at);
+
+  const int n = int(gridDim.x), per = n / kXcds, rem = n % kXcds;
+  const int xcd = int(blockIdx.x) % kXcds, slot = int(blockIdx.x) / kXcds;
+  const int blk = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  const int chunk = blk % gp.nchunks;
+  const int bh = blk / gp.nchunks;
+  const int h = bh % p.H, b = bh / p.H;
+  const int p0 = chunk * npos;
+  const int p1 = min(p0 + npos, p.S);
+  const int LP = p.L * p.P;
+
+  load_levels(p, levels);
+  for (int i = tid; i < npos; i += nthreads) cnt[i] = 0;
+
+  A accum[kItemsPerThread][CVR];
+#pragma unroll
+  for (int k = 0; k < kItemsPerThread; ++k)
+#pragma unroll
+    for (int c = 0; c < CVR; ++c) accum[k][c] = A(0);
+  __syncthreads();
+
+  const T* gout = reinterpret_cast<const T*>(p.grad_out);
+  const T* attn_all = reinterpret_cast<const T*>(p.attn);
+  const TL* loc_all = reinterpret_cast<const TL*>(p.loc);
+  const int P2 = 1 << gp.p2_log2;
+  const int tile = qb * p.D;  // elements of one block's grad_out tile
+  constexpr int kVec = 16 / ES;
+
+  for (int l = 0; l < p.L; ++l) {
+    const Level lv = levels[l];
+    if (!lv.ok) continue;
+    const int a0 = max(p0, lv.start), a1 = min(p1, lv.start + lv.h * lv.w);
+    if (a0 >= a1) continue;  // uniform across the workgroup
+    const int row_lo = (a0 - lv.start) / lv.w, row_hi = (a1 - 1 - lv.start) / lv.w;
+    const RowRange* lrows = rows + ((int64_t(b) * p.H + h) * p.L + l) * gp.nblocks;
+    for (int jb = 0; jb < gp.nblocks; jb += nthreads) {
+      // Select the blocks of this round whose rows reach the chunk.
+      bool reach = false;
+      if (jb + tid < gp.nblocks) {
+        const RowRange rr = lrows[jb + tid];
+        reach = rr.hi >= row_lo && rr.lo <= row_hi;
+      }
+      int nsel;
+      const int at_sel = block_exclusive_scan(reach ? 1 : 0, wave_sums, &nsel);
+      if (reach) blist[at_sel] = jb + tid;
+      __syncthreads();
+      for (int s0 = 0; s0 < nsel; s0 += nwaves) {
+        // A. One block per wave: records in registers (one slot per corner, so the
+        // arrays stay in VGPRs), grad_out tile in LDS.
+        bool rv[4] = {false, false, false, false};
+        uint32_t rpos[4] = {0u, 0u, 0u, 0u};
+        A rw[4] = {A(0), A(0), A(0), A(0)};
+        const bool has_block = s0 + wave < nsel;
+        const int j = has_block ? blist[s0 + wave] : 0;
+        const int q0 = j * qb;
+        const int qn = has_block ? min(qb, p.Q - q0) : 0;
+        T* wtile = gtile + size_t(wave) * tile;
+        if (has_block) {
+          const BlockSlot bs = block_slot(p, gp.p2_log2, j, lane);
+          const int s = l * p.P + bs.pt;
+          const int64_t unit = (int64_t(b) * p.Q + (bs.q < p.Q ? bs.q : q0)) * p.H + h;
+          A lx = A(0), ly = A(0), a = A(0);
+          if (bs.ok) {
+            const TL* lc = loc_all + (unit * LP + s) * 2;
+            lx = load_acc(lc);
+            ly = load_acc(lc + 1);
+            if constexpr (!SOFTMAX) a = load_acc(attn_all + unit * LP + s);
+          }
+          // The grad_out tile: QB vectors of D elements, CVR-aligned pieces.
+          for (int e = lane * kVec; e < qn * p.D; e += kWave * kVec) {
+            const int qi = e / p.D, c = e - qi * p.D;
+            const T* src = gout + ((int64_t(b) * p.Q + q0 + qi) * p.H + h) * p.D + c;
+            if ((p.D % kVec) == 0 && (reinterpret_cast<uintptr_t>(gout) & 15) == 0) {
+              *reinterpret_cast<uint4*>(wtile + e) = *reinterpret_cast<const uint4*>(src);
+            } else {
+              for (int v = 0; v < kVec && e + v < qn * p.D; ++v) {
+                const int qv = (e + v) / p.D, cv = (e + v) - qv * p.D;
+                wtile[e + v] = gout[((int64_t(b) * p.Q + q0 + qv) * p.H + h) * p.D + cv];
+              }
+            }
+          }
+          if constexpr (SOFTMAX) {
+            // The P2 lanes of a query share its L * P logits: max, then sum of exp.
+            const T* ua = attn_all + unit * LP;
+            A mx = -INFINITY;
+            if (bs.q < p.Q)
+              for (int i = bs.pt; i < LP; i += P2) mx = fmax(mx, load_acc(ua + i));
+            for (int m2 = 1; m2 < P2; m2 <<= 1) mx = fmax(mx, __shfl_xor(mx, m2, kWave));
+            A sum(0);
+            if (bs.q < p.Q)
+              for (int i = bs.pt; i < LP; i += P2) sum += exp_acc(load_acc(ua + i) - mx);
+            for (int m2 = 1; m2 < P2; m2 <<= 1) sum += __shfl_xor(sum, m2, kWave);
+            if (bs.ok) a = exp_acc(load_acc(ua + s) - mx) / sum;
+          }
+          if (bs.ok) {
+            const Geom<A> g = geometry<A>(lx, ly, lv, 0u, 1u);
+            const bool m[4] = {g.m00, g.m01, g.m10, g.m11};
+            const A wb[4] = {g.w00, g.w01, g.w10, g.w11};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              rv[c] = m[c] && int(g.off[c]) >= a0 && int(g.off[c]) < a1;
+              rpos[c] = g.off[c] - uint32_t(p0);
+              rw[c] = wb[c] * a;
+            }
+          }
+        }
+        // B. Histogram.
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (rv[c]) atomicAdd(&cnt[rpos[c]], 1);
+        __syncthreads();
+        // C. Start of every position's run.
+        {
+          int total;
+          const int v = tid < npos ? cnt[tid] : 0;
+          const int ex = block_exclusive_scan(v, wave_sums, &total);
+          if (tid < npos) {
+            start[tid] = ex;
+            cursor[tid] = ex;
+          }
+          if (tid == 0) start[npos] = total;
+        }
+        __syncthreads();
+        // D. Place the records.
+        const uint32_t qslot = uint32_t(wave * qb + (lane >> gp.p2_log2));
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (rv[c]) {
+            const int dst = atomicAdd(&cursor[rpos[c]], 1);
+            sorted[dst] = SortedRec<A>{rw[c], qslot};
+          }
+        }
+        __syncthreads();
+        // E. Accumulate the runs of the owned items.
+#pragma unroll
+        for (int k = 0; k < kItemsPerThread; ++k) {
+          const int item = tid + k * nthreads;
+          const int pos = item / gp.groups, grp = item - pos * gp.groups;
+          if (pos < npos) {
+            const int r1 = start[pos + 1];
+            for (int r = start[pos]; r < r1; ++r) {
+              const SortedRec<A> rec = sorted[r];
+              const T* gq = gtile + size_t(rec.qslot) * p.D + grp * CVR;
+              A gv[CVR];
+              Chan<T, CVR>::load(reinterpret_cast<const char*>(gq), gv);
+#pragma unroll
+              for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec.w, gv[c], accum[k][c]);
+            }
+          }
+        }
+        for (int i = tid; i < npos; i += nthreads) cnt[i] = 0;
+        __syncthreads();
+      }
+    }
+  }
+
+  // Write the owned items: the only writer of these grad_value elements.
+  T* gv_out = reinterpret_cast<T*>(p.grad_value);
+  const int64_t img = int64_t(b) * p.S * p.H * p.D;
+#pragma unroll
+  for (int k = 0; k < kItemsPerThread; ++k) {
+    const int item = tid + k * nthreads;
+    const int pos = item / gp.groups, grp = item - pos * gp.groups;
+    if (pos < p1 - p0) {
+      char* dst = reinterpret_cast<char*>(gv_out + img + (int64_t(p0 + pos) * p.H + h) * p.D + grp * CVR);
+      if (accumulate) {
+        A old[CVR];
+        Chan<T, CVR>::load(dst, old);
+#pragma unroll
+        for (int c = 0; c < CVR; ++c) accum[k][c] += old[c];
+      }
+      Chan<T, CVR>::store(dst, accum[k]);
+    }
+  }
+}
+
+// Location and weight gradients, sample-parallel, laid out like the forward.
 template <typename T, typename TL, int CV, bool SOFTMAX>
-__global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_backward_kernel(const Problem p) {
+__global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_kernel(const Problem p) {
   using A = typename Elem<T>::acc;
   constexpr int ES = Elem<T>::size;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -456,11 +837,10 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_backward_kerne
   stage_samples<T, TL, SOFTMAX>(p, m, levels, wst, smax, sinv);
   __syncthreads();
 
-  // Phase 2: gather, corner dot products, atomic scatter into grad_value.
+  // Gather the corners and form G_c; the lane that staged sample s keeps its G_c
+  // in the sample's slot.
   const bool lane_ok = m.unit_ok && m.t * CV < p.D;
-  const int64_t img_off = int64_t(m.b) * p.S * p.H * p.D * ES;
-  const char* img = p.value + img_off;
-  char* gimg = p.grad_value + img_off;
+  const char* img = p.value + int64_t(m.b) * p.S * p.H * p.D * ES;
   const uint32_t lane_bytes = uint32_t(m.t * CV * ES);
   A g[CV];
   if (lane_ok) {
@@ -488,15 +868,9 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_backward_kerne
 #pragma unroll
       for (int c = 0; c < 4; ++c) slot->w[c] = G[c];
     }
-    if (lane_ok) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (st.w[c] != A(0)) Chan<T, CV>::atomic_add(gimg + (st.off[c] + lane_bytes), g, st.w[c]);
-    }
   }
 
-  // Phase 3: per-sample location and weight gradients, by the lane that staged
-  // the sample (it alone wrote the sample's G_c back into its slot).
+  // Per-sample location and weight gradients by the lane that staged the sample.
   const TL* loc = reinterpret_cast<const TL*>(p.loc) + m.gunit * LP * 2;
   const T* attn = reinterpret_cast<const T*>(p.attn) + m.gunit * LP;
   TL* gloc = reinterpret_cast<TL*>(p.grad_loc) + m.gunit * LP * 2;
@@ -517,16 +891,16 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_backward_kerne
       const A G10 = ge.m10 ? slot->w[2] : A(0);
       const A G11 = ge.m11 ? slot->w[3] : A(0);
       const A one(1);
-      const A gp = ge.w00 * G00 + ge.w01 * G01 + ge.w10 * G10 + ge.w11 * G11;
+      const A gpv = ge.w00 * G00 + ge.w01 * G01 + ge.w10 * G10 + ge.w11 * G11;
       const A gx = a * A(lv.w) * ((one - ge.dy) * (G01 - G00) + ge.dy * (G11 - G10));
       const A gy = a * A(lv.h) * ((one - ge.dx) * (G10 - G00) + ge.dx * (G11 - G01));
       store_elem(gloc + 2 * s, gx);
       store_elem(gloc + 2 * s + 1, gy);
       if constexpr (SOFTMAX) {
-        dot += a * gp;
-        slot->w[0] = gp;
+        dot += a * gpv;
+        slot->w[0] = gpv;
       } else {
-        store_elem(gattn + s, gp);
+        store_elem(gattn + s, gpv);
       }
     }
   }
@@ -535,15 +909,15 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_backward_kerne
     if (m.unit_ok) {
       for (int s = m.t; s < LP; s += m.lh) {
         const A a = exp_acc(load_acc(attn + s) - smax) * sinv;
-        const A gp = wst[s * m.uw_count + m.uw].w[0];
-        store_elem(gattn + s, a * (gp - dot));
+        const A gpv = wst[s * m.uw_count + m.uw].w[0];
+        store_elem(gattn + s, a * (gpv - dot));
       }
     }
   }
 }
 
-// Zero-fill of grad_value before the atomics: a plain kernel (not hipMemsetAsync),
-// so a caller may capture the backward in a HIP graph.
+// Zero-fill for empty calls: a plain kernel (not hipMemsetAsync), so a caller may
+// capture the call in a HIP graph.
 __global__ __launch_bounds__(256) void zero_fill_kernel(char* p, int64_t bytes) {
   const uintptr_t a = reinterpret_cast<uintptr_t>(p);
   const int64_t head = int64_t((16 - (a & 15)) & 15) < bytes ? int64_t((16 - (a & 15)) & 15) : bytes;
@@ -666,59 +1040,163 @@ int make_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, 
   return MSDA_OK;
 }
 
-template <bool BWD, typename T, typename TL, int CV>
-hipError_t launch_cv(const Problem& p, const Plan& plan, int softmax, hipStream_t stream) {
-  const dim3 grid(unsigned(plan.num_blocks)), block(unsigned(kWave * plan.waves));
-  if constexpr (BWD) {
-    if (softmax)
-      hipLaunchKernelGGL((msda_backward_kernel<T, TL, CV, true>), grid, block, plan.lds, stream, p);
-    else
-      hipLaunchKernelGGL((msda_backward_kernel<T, TL, CV, false>), grid, block, plan.lds, stream, p);
-  } else {
-    if (softmax)
-      hipLaunchKernelGGL((msda_forward_kernel<T, TL, CV, true>), grid, block, plan.lds, stream, p);
-    else
-      hipLaunchKernelGGL((msda_forward_kernel<T, TL, CV, false>), grid, block, plan.lds, stream, p);
-  }
-  return hipGetLastError();
-}
-
-template <bool BWD, typename T, typename TL>
-hipError_t launch_tl(const Problem& p, const Plan& plan, int softmax, hipStream_t stream) {
+// Dispatch on (value dtype, location dtype, channels per lane): f is a generic
+// lambda taking <T, TL, CV> template arguments.
+template <typename T, typename TL, typename F>
+hipError_t dispatch_cv(int cv, F& f) {
   constexpr int kMaxCv = 16 / Elem<T>::size;
-  switch (plan.cv) {
-    case 1: return launch_cv<BWD, T, TL, 1>(p, plan, softmax, stream);
-    case 2: return launch_cv<BWD, T, TL, 2>(p, plan, softmax, stream);
+  switch (cv) {
+    case 1: return f.template operator()<T, TL, 1>();
+    case 2: return f.template operator()<T, TL, 2>();
     case 4:
-      if constexpr (kMaxCv >= 4) return launch_cv<BWD, T, TL, 4>(p, plan, softmax, stream);
+      if constexpr (kMaxCv >= 4) return f.template operator()<T, TL, 4>();
       break;
     case 8:
-      if constexpr (kMaxCv >= 8) return launch_cv<BWD, T, TL, 8>(p, plan, softmax, stream);
+      if constexpr (kMaxCv >= 8) return f.template operator()<T, TL, 8>();
       break;
   }
   return hipErrorInvalidValue;
 }
 
-template <bool BWD, typename T>
-hipError_t launch_t(const Problem& p, const Plan& plan, int loc_f32, int softmax, hipStream_t stream) {
-  if constexpr (__is_same(T, float) || __is_same(T, double)) {
-    return launch_tl<BWD, T, T>(p, plan, softmax, stream);
-  } else {
-    return loc_f32 ? launch_tl<BWD, T, float>(p, plan, softmax, stream)
-                   : launch_tl<BWD, T, T>(p, plan, softmax, stream);
-  }
-}
-
-template <bool BWD>
-hipError_t launch(int dtype, const Problem& p, const Plan& plan, int loc_f32, int softmax,
-                  hipStream_t stream) {
+template <typename F>
+hipError_t dispatch(int dtype, bool loc_f32, int cv, F&& f) {
   switch (dtype) {
-    case MSDA_F32: return launch_t<BWD, float>(p, plan, loc_f32, softmax, stream);
-    case MSDA_F64: return launch_t<BWD, double>(p, plan, loc_f32, softmax, stream);
-    case MSDA_BF16: return launch_t<BWD, bf16_t>(p, plan, loc_f32, softmax, stream);
-    case MSDA_F16: return launch_t<BWD, f16_t>(p, plan, loc_f32, softmax, stream);
+    case MSDA_F32: return dispatch_cv<float, float>(cv, f);
+    case MSDA_F64: return dispatch_cv<double, double>(cv, f);
+    case MSDA_BF16:
+      return loc_f32 ? dispatch_cv<bf16_t, float>(cv, f) : dispatch_cv<bf16_t, bf16_t>(cv, f);
+    case MSDA_F16:
+      return loc_f32 ? dispatch_cv<f16_t, float>(cv, f) : dispatch_cv<f16_t, f16_t>(cv, f);
   }
   return hipErrorInvalidValue;
+}
+
+// Launch layout of the backward's three kernels.
+struct BackwardPlan {
+  GradValuePlan gv;
+  int gv_threads;
+  int cvr;
+  size_t gv_lds;
+  int64_t gv_blocks;
+  int64_t summary_entries;
+  Plan sample;
+};
+
+size_t device_lds_limit() {
+  int dev = 0, bytes = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+      bytes <= 0)
+    return 64 * 1024;
+  return size_t(bytes);
+}
+
+size_t grad_value_lds(int dtype, int threads, int64_t L, int64_t D, int qb, int64_t npos) {
+  const size_t es = size_t(elem_size(dtype));
+  const size_t rec = dtype == MSDA_F64 ? sizeof(SortedRec<double>) : sizeof(SortedRec<float>);
+  const size_t waves = size_t(threads / kWave);
+  size_t at = sizeof(Level) * size_t(L);
+  at += rec * waves * kRecordsPerWave;
+  at += (es * waves * size_t(qb) * size_t(D) + 15) & ~size_t(15);
+  at += sizeof(int) * (3 * size_t(npos) + 1);
+  at += sizeof(int) * size_t(threads);
+  at += sizeof(int) * waves;
+  return at;
+}
+
+int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, int64_t L,
+                       int64_t P, int loc_dtype, const void* const* vec_ptrs, int n_vec,
+                       size_t lds_limit, BackwardPlan* plan) {
+  int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_vec, &plan->sample);
+  if (rc != MSDA_OK) return rc;
+  if (P > kWave)
+    return fail(MSDA_ERR_UNSUPPORTED, "msda: the backward takes at most %d points per level", kWave);
+  int p2_log2 = 0;
+  while ((int64_t(1) << p2_log2) < P) ++p2_log2;
+  const int qb = kWave >> p2_log2;
+  const int64_t nblocks = (Q + qb - 1) / qb;
+  const int64_t entries = B * H * L * nblocks;
+  const int64_t loc_bytes = B * Q * H * L * P * 2 * elem_size(loc_dtype);
+  if (entries * int64_t(sizeof(RowRange)) > loc_bytes)
+    return fail(MSDA_ERR_UNSUPPORTED, "msda: row summaries do not fit the location gradient");
+  // Channels per register item: the widest power of two that divides D, fits a
+  // 16-byte access and keeps grad_value aligned to it.
+  const int es = elem_size(dtype);
+  int cvr = 16 / es;
+  while (cvr > 1) {
+    bool ok = D % cvr == 0;
+    for (int i = 0; i < n_vec && ok; ++i) ok = aligned(vec_ptrs[i], cvr * es);
+    if (ok) break;
+    cvr >>= 1;
+  }
+  const int64_t groups = D / cvr;
+  const size_t budget = lds_limit < 160 * 1024 ? lds_limit : 160 * 1024;
+  int threads = kGradValueMaxThreads;
+  int64_t npos = 0;
+  for (;;) {
+    npos = std::min<int64_t>({int64_t(threads), int64_t(threads) * kItemsPerThread / groups, S});
+    if (npos >= 1 && grad_value_lds(dtype, threads, L, D, qb, npos) <= budget) break;
+    if (threads == kWave)
+      return fail(MSDA_ERR_UNSUPPORTED,
+                  "msda: %lld channels per head do not fit the backward's register and LDS budget",
+                  (long long)D);
+    threads >>= 1;
+  }
+  const int64_t nchunks = (S + npos - 1) / npos;
+  const int64_t blocks = B * H * nchunks;
+  if (blocks >= 2147483647 || nblocks >= 2147483647 || entries * kWave >= (int64_t(1) << 40))
+    return fail(MSDA_ERR_UNSUPPORTED, "msda: backward grid too large");
+  plan->gv = GradValuePlan{int(npos), int(nchunks), p2_log2, int(nblocks), int(groups)};
+  plan->gv_threads = threads;
+  plan->cvr = cvr;
+  plan->gv_lds = grad_value_lds(dtype, threads, L, D, qb, npos);
+  plan->gv_blocks = blocks;
+  plan->summary_entries = entries;
+  return MSDA_OK;
+}
+
+template <typename T, typename TL, bool SOFTMAX>
+hipError_t launch_grad_value(const BackwardPlan& plan, const Problem& p, const RowRange* rows,
+                             int accumulate, hipStream_t st) {
+  constexpr int kMaxCv = 16 / Elem<T>::size;
+  const void* fn = nullptr;
+  switch (plan.cvr) {
+    case 1: fn = reinterpret_cast<const void*>(msda_grad_value_kernel<T, TL, 1, SOFTMAX>); break;
+    case 2: fn = reinterpret_cast<const void*>(msda_grad_value_kernel<T, TL, 2, SOFTMAX>); break;
+    case 4:
+      if constexpr (kMaxCv >= 4) fn = reinterpret_cast<const void*>(msda_grad_value_kernel<T, TL, 4, SOFTMAX>);
+      break;
+    case 8:
+      if constexpr (kMaxCv >= 8) fn = reinterpret_cast<const void*>(msda_grad_value_kernel<T, TL, 8, SOFTMAX>);
+      break;
+  }
+  if (!fn) return hipErrorInvalidValue;
+  if (plan.gv_lds > 64 * 1024) {
+    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(plan.gv_lds));
+    if (e != hipSuccess) return e;
+  }
+  const dim3 grid(unsigned(plan.gv_blocks)), block(unsigned(plan.gv_threads));
+  switch (plan.cvr) {
+    case 1:
+      hipLaunchKernelGGL((msda_grad_value_kernel<T, TL, 1, SOFTMAX>), grid, block, plan.gv_lds, st, p,
+                         plan.gv, rows, accumulate);
+      break;
+    case 2:
+      hipLaunchKernelGGL((msda_grad_value_kernel<T, TL, 2, SOFTMAX>), grid, block, plan.gv_lds, st, p,
+                         plan.gv, rows, accumulate);
+      break;
+    case 4:
+      if constexpr (kMaxCv >= 4)
+        hipLaunchKernelGGL((msda_grad_value_kernel<T, TL, 4, SOFTMAX>), grid, block, plan.gv_lds, st, p,
+                           plan.gv, rows, accumulate);
+      break;
+    case 8:
+      if constexpr (kMaxCv >= 8)
+        hipLaunchKernelGGL((msda_grad_value_kernel<T, TL, 8, SOFTMAX>), grid, block, plan.gv_lds, st, p,
+                           plan.gv, rows, accumulate);
+      break;
+  }
+  return hipGetLastError();
 }
 
 int check_call(int value_dtype, int index_dtype, int loc_dtype, int64_t B, int64_t S, int64_t H,
@@ -795,9 +1273,24 @@ int msda_launch_geometry(int value_dtype, int64_t batch, int64_t spatial, int64_
                          int64_t channels, int64_t queries, int64_t levels, int64_t points,
                          int backward, int* channels_per_lane, int* lanes_per_unit,
                          int* waves_per_block, int64_t* num_blocks) {
+  if (elem_size(value_dtype) == 0)
+    return fail(MSDA_ERR_INVALID, "msda: unknown value dtype code %d", value_dtype);
+  if (backward) {
+    BackwardPlan bp;
+    const int rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries,
+                                      levels, points, value_dtype, nullptr, 0, 160 * 1024, &bp);
+    if (rc != MSDA_OK) return rc;
+    // The grad_value kernel's layout: channels per register item, positions per
+    // chunk, waves per workgroup and workgroups.
+    if (channels_per_lane) *channels_per_lane = bp.cvr;
+    if (lanes_per_unit) *lanes_per_unit = bp.gv.npos;
+    if (waves_per_block) *waves_per_block = bp.gv_threads / kWave;
+    if (num_blocks) *num_blocks = bp.gv_blocks;
+    return MSDA_OK;
+  }
   Plan plan;
   const int rc = make_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
-                           backward != 0, nullptr, 0, &plan);
+                           false, nullptr, 0, &plan);
   if (rc != MSDA_OK) return rc;
   if (channels_per_lane) *channels_per_lane = plan.cv;
   if (lanes_per_unit) *lanes_per_unit = 1 << plan.lh_log2;
@@ -833,8 +1326,17 @@ int msda_forward(const void* value, int value_dtype, const void* spatial_shapes,
                            sampling_locations, attention_weights, batch, spatial, heads,
                            channels, queries, levels, points, plan);
   p.out = static_cast<char*>(output);
-  const hipError_t err = launch<false>(value_dtype, p, plan, loc_dtype == MSDA_F32,
-                                       flags & MSDA_SOFTMAX, st);
+  const bool softmax = flags & MSDA_SOFTMAX;
+  const hipError_t err = dispatch(
+      value_dtype, loc_dtype == MSDA_F32 && value_dtype != MSDA_F32, plan.cv,
+      [&]<typename T, typename TL, int CV>() {
+        const dim3 grid(unsigned(plan.num_blocks)), block(unsigned(kWave * plan.waves));
+        if (softmax)
+          hipLaunchKernelGGL((msda_forward_kernel<T, TL, CV, true>), grid, block, plan.lds, st, p);
+        else
+          hipLaunchKernelGGL((msda_forward_kernel<T, TL, CV, false>), grid, block, plan.lds, st, p);
+        return hipGetLastError();
+      });
   if (err != hipSuccess)
     return fail(MSDA_ERR_HIP, "msda_forward: launch failed: %s", hipGetErrorString(err));
   return MSDA_OK;
@@ -858,14 +1360,16 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
     return fail(MSDA_ERR_INVALID, "msda_backward: null grad_value");
   if (sample_count > 0 && (!grad_sampling_locations || !grad_attention_weights))
     return fail(MSDA_ERR_INVALID, "msda_backward: null location or weight gradient");
+  const bool accumulate = flags & MSDA_ACCUMULATE_GRAD_VALUE;
   (void)hipGetLastError();
-  if (value_bytes > 0 && !(flags & MSDA_ACCUMULATE_GRAD_VALUE)) {
-    rc = zero_fill(grad_value, value_bytes, st, "msda_backward");
-    if (rc != MSDA_OK) return rc;
-  }
-  if (sample_count == 0) return MSDA_OK;
-  if (channels == 0 || spatial == 0) {
-    // Nothing to sample from: every location and weight gradient is zero.
+  if (sample_count == 0 || channels == 0 || spatial == 0) {
+    // Nothing to sample: grad_value keeps its contents (accumulate) or becomes zero,
+    // and every location and weight gradient is zero.
+    if (value_bytes > 0 && !accumulate) {
+      rc = zero_fill(grad_value, value_bytes, st, "msda_backward");
+      if (rc != MSDA_OK) return rc;
+    }
+    if (sample_count == 0) return MSDA_OK;
     rc = zero_fill(grad_sampling_locations, sample_count * 2 * elem_size(loc_dtype), st,
                    "msda_backward");
     if (rc != MSDA_OK) return rc;
@@ -874,20 +1378,42 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
       !attention_weights || !grad_output)
     return fail(MSDA_ERR_INVALID, "msda_backward: null input tensor pointer");
+  if (reinterpret_cast<uintptr_t>(grad_sampling_locations) % alignof(RowRange) != 0)
+    return fail(MSDA_ERR_INVALID, "msda_backward: grad_sampling_locations must be 4-byte aligned");
   const void* vec[] = {value, grad_output, grad_value};
-  Plan plan;
-  rc = make_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points, true,
-                 vec, 3, &plan);
+  BackwardPlan plan;
+  rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
+                          loc_dtype, vec, 2, device_lds_limit(), &plan);
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,
-                           channels, queries, levels, points, plan);
+                           channels, queries, levels, points, plan.sample);
   p.grad_out = static_cast<const char*>(grad_output);
   p.grad_value = static_cast<char*>(grad_value);
   p.grad_loc = static_cast<char*>(grad_sampling_locations);
   p.grad_attn = static_cast<char*>(grad_attention_weights);
-  const hipError_t err = launch<true>(value_dtype, p, plan, loc_dtype == MSDA_F32,
-                                      flags & MSDA_SOFTMAX, st);
+  RowRange* rows = static_cast<RowRange*>(grad_sampling_locations);
+  const bool softmax = flags & MSDA_SOFTMAX;
+  const hipError_t err = dispatch(
+      value_dtype, loc_dtype == MSDA_F32 && value_dtype != MSDA_F32, plan.sample.cv,
+      [&]<typename T, typename TL, int CV>() {
+        const unsigned summary_blocks = unsigned((plan.summary_entries * kWave + 255) / 256);
+        hipLaunchKernelGGL((msda_row_summary_kernel<T, TL>), dim3(summary_blocks), dim3(256), 0, st,
+                           p, plan.gv, rows);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        e = softmax ? launch_grad_value<T, TL, true>(plan, p, rows, int(accumulate), st)
+                    : launch_grad_value<T, TL, false>(plan, p, rows, int(accumulate), st);
+        if (e != hipSuccess) return e;
+        const dim3 grid(unsigned(plan.sample.num_blocks)), block(unsigned(kWave * plan.sample.waves));
+        if (softmax)
+          hipLaunchKernelGGL((msda_grad_sample_kernel<T, TL, CV, true>), grid, block,
+                             plan.sample.lds, st, p);
+        else
+          hipLaunchKernelGGL((msda_grad_sample_kernel<T, TL, CV, false>), grid, block,
+                             plan.sample.lds, st, p);
+        return hipGetLastError();
+      });
   if (err != hipSuccess)
     return fail(MSDA_ERR_HIP, "msda_backward: launch failed: %s", hipGetErrorString(err));
   return MSDA_OK;
