@@ -524,14 +524,24 @@ __device__ inline typename Elem<T>::acc unit_weight(const T* unit_attn, int LP, 
   }
 }
 
-// Inclusive prefix sum of v over the wave.
+// Workgroup barrier for LDS traffic only: the fences are restricted to the local
+// address space, so global loads issued before it stay in flight across it.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// Inclusive prefix sum of v over the wave with DPP lane moves (VALU, no LDS round
+// trips): shifts by 1, 2, 4, 8 inside each row of 16 lanes, then row broadcasts of
+// lane 15 and lane 31 carry the row totals forward.
 __device__ inline int wave_inclusive_scan(int v) {
-  const int lane = threadIdx.x & (kWave - 1);
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    const int y = __shfl_up(v, d, kWave);
-    if (lane >= d) v += y;
-  }
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
   return v;
 }
 
@@ -542,14 +552,14 @@ __device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
   const int nwaves = int(blockDim.x) / kWave;
   const int inc = wave_inclusive_scan(v);
   if (lane == kWave - 1) wave_sums[wave] = inc;
-  __syncthreads();
+  lds_barrier();
   int before = 0, all = 0;
   for (int w = 0; w < nwaves; ++w) {
     const int ws = wave_sums[w];
     before += w < wave ? ws : 0;
     all += ws;
   }
-  __syncthreads();
+  lds_barrier();
   *total = all;
   return before + inc - v;
 }
@@ -615,6 +625,66 @@ __global__ __launch_bounds__(256) void msda_row_summary_kernel(const Problem p, 
   if (lane == 0) out[e] = RowRange{lo, hi};
 }
 
+// Raw (unconverted) element types, so that a prefetch does not wait for its data.
+__device__ inline float to_acc(float v) { return v; }
+__device__ inline double to_acc(double v) { return v; }
+__device__ inline float to_acc(bf16_t v) { return __uint_as_float(uint32_t(v.bits) << 16); }
+__device__ inline float to_acc(f16_t v) { return f16_bits(v.bits); }
+
+template <typename TL> struct LocPair {
+  TL x, y;
+};
+
+// Register copy of what one wave needs from global memory for one query block:
+// the lane's location pair and weight, and one 16-byte piece of the block's
+// grad_out tile. Kept raw and converted at use, so the loads of the next block stay
+// in flight while the current one is processed.
+template <typename T, typename TL> struct BlockFetch {
+  bool has;
+  int j;
+  LocPair<TL> loc;
+  T a;
+  uint4 tv;
+};
+
+// Branch-free: every lane issues the same three loads (from clamped, always valid
+// addresses) and selects afterwards, so the compiler can count them and leave them in
+// flight while the previous block is processed.
+template <typename T, typename TL, bool SOFTMAX>
+__device__ inline BlockFetch<T, TL> fetch_block(const Problem& p, const GradValuePlan& gp, int sidx,
+                                                int nsel, const int* blist, int l, int b, int h,
+                                                const TL* loc_all, const T* attn_all, const T* gout,
+                                                bool tile_vec) {
+  constexpr int kVec = 16 / Elem<T>::size;
+  const int lane = threadIdx.x & (kWave - 1);
+  BlockFetch<T, TL> f;
+  f.has = sidx < nsel;
+  // blist[0] is a block of this round only when nsel > 0; otherwise read block 0,
+  // which exists whenever the kernel runs (Q > 0). Clamped, so every address below
+  // stays inside the tensors whatever the LDS holds.
+  const int jj = f.has ? blist[sidx] : (nsel > 0 ? blist[0] : 0);
+  f.j = min(max(jj, 0), gp.nblocks - 1);
+  const int qb = kWave >> gp.p2_log2;
+  const int q0 = f.j * qb;
+  const int qn = min(qb, p.Q - q0);
+  const BlockSlot bs = block_slot(p, gp.p2_log2, f.j, lane);
+  const int LP = p.L * p.P;
+  const int q = bs.ok ? bs.q : q0;
+  const int s = l * p.P + (bs.ok ? bs.pt : 0);
+  const int64_t unit = (int64_t(b) * p.Q + q) * p.H + h;
+  f.loc = *reinterpret_cast<const LocPair<TL>*>(loc_all + (unit * LP + s) * 2);
+  if constexpr (!SOFTMAX) f.a = attn_all[unit * LP + s];
+  else f.a = T{};
+  int e = lane * kVec;
+  if (!(tile_vec && e < qn * p.D)) e = 0;
+  const int qi = e / p.D, c = e - qi * p.D;
+  if (tile_vec)
+    f.tv = *reinterpret_cast<const uint4*>(gout + ((int64_t(b) * p.Q + q0 + qi) * p.H + h) * p.D + c);
+  else
+    f.tv = make_uint4(0, 0, 0, 0);
+  return f;
+}
+
 template <typename T, typename TL, int CVR, bool SOFTMAX>
 __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
     const Problem p, const GradValuePlan gp, const RowRange* __restrict__ rows, const int accumulate) {
@@ -643,11 +713,17 @@ __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
   int* blist = reinterpret_cast<int*>(smem + at);  // selected blocks, one per thread
   at += sizeof(int) * size_t(nthreads);
   int* wave_sums = reinterpret_cast<int*>(smem + at);
+  at += (sizeof(int) * size_t(nwaves) + 15) & ~size_t(15);
+  LocPair<TL>* sloc = reinterpret_cast<LocPair<TL>*>(smem + at);  // per lane: the staged location
+  at += sizeof(LocPair<TL>) * size_t(nthreads);
+  T* sattn = reinterpret_cast<T*>(smem + at);  // per lane: the staged weight
 
   const int n = int(gridDim.x), per = n / kXcds, rem = n % kXcds;
   const int xcd = int(blockIdx.x) % kXcds, slot = int(blockIdx.x) / kXcds;
   const int blk = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
-  const int chunk = blk % gp.nchunks;
+  // Last chunks first: with pyramids stored fine to coarse they hold the coarse,
+  // most sampled levels, so the longest workgroups start earliest.
+  const int chunk = gp.nchunks - 1 - blk % gp.nchunks;
   const int bh = blk / gp.nchunks;
   const int h = bh % p.H, b = bh / p.H;
   const int p0 = chunk * npos;
@@ -670,6 +746,8 @@ __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
   const int P2 = 1 << gp.p2_log2;
   const int tile = qb * p.D;  // elements of one block's grad_out tile
   constexpr int kVec = 16 / ES;
+  const bool tile_vec = (p.D % kVec) == 0 && (reinterpret_cast<uintptr_t>(gout) & 15) == 0 &&
+                        tile <= kWave * kVec;
 
   for (int l = 0; l < p.L; ++l) {
     const Level lv = levels[l];
@@ -688,15 +766,33 @@ __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
       int nsel;
       const int at_sel = block_exclusive_scan(reach ? 1 : 0, wave_sums, &nsel);
       if (reach) blist[at_sel] = jb + tid;
-      __syncthreads();
+      lds_barrier();
+      if (nsel == 0) continue;  // uniform across the workgroup
+      // Each wave's current block lives in LDS: its lanes' location pairs and
+      // weights, and the block's grad_out tile. The next block's global loads are
+      // issued at the start of a batch and written to LDS only after the batch's
+      // last barrier, so they stay in flight while the batch is processed.
+      bool cur_has;
+      int cur_j;
+      {
+        const BlockFetch<T, TL> first = fetch_block<T, TL, SOFTMAX>(p, gp, wave, nsel, blist, l, b, h,
+                                                                    loc_all, attn_all, gout, tile_vec);
+        sloc[tid] = first.loc;
+        sattn[tid] = first.a;
+        if (tile_vec && lane * kVec < tile) *reinterpret_cast<uint4*>(gtile + size_t(wave) * tile + lane * kVec) = first.tv;
+        cur_has = first.has;
+        cur_j = first.j;
+      }
       for (int s0 = 0; s0 < nsel; s0 += nwaves) {
+        const BlockFetch<T, TL> nxt = fetch_block<T, TL, SOFTMAX>(p, gp, s0 + nwaves + wave, nsel, blist,
+                                                                  l, b, h, loc_all, attn_all, gout, tile_vec);
         // A. One block per wave: records in registers (one slot per corner, so the
-        // arrays stay in VGPRs), grad_out tile in LDS.
+        // arrays stay in VGPRs).
         bool rv[4] = {false, false, false, false};
         uint32_t rpos[4] = {0u, 0u, 0u, 0u};
         A rw[4] = {A(0), A(0), A(0), A(0)};
-        const bool has_block = s0 + wave < nsel;
-        const int j = has_block ? blist[s0 + wave] : 0;
+        const bool has_block = cur_has;
+        const int j = cur_j;
         const int q0 = j * qb;
         const int qn = has_block ? min(qb, p.Q - q0) : 0;
         T* wtile = gtile + size_t(wave) * tile;
@@ -704,27 +800,15 @@ __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
           const BlockSlot bs = block_slot(p, gp.p2_log2, j, lane);
           const int s = l * p.P + bs.pt;
           const int64_t unit = (int64_t(b) * p.Q + (bs.q < p.Q ? bs.q : q0)) * p.H + h;
-          A lx = A(0), ly = A(0), a = A(0);
-          if (bs.ok) {
-            const TL* lc = loc_all + (unit * LP + s) * 2;
-            lx = load_acc(lc);
-            ly = load_acc(lc + 1);
-            if constexpr (!SOFTMAX) a = load_acc(attn_all + unit * LP + s);
-          }
-          // The grad_out tile: QB vectors of D elements, CVR-aligned pieces.
-          for (int e = lane * kVec; e < qn * p.D; e += kWave * kVec) {
-            const int qi = e / p.D, c = e - qi * p.D;
-            const T* src = gout + ((int64_t(b) * p.Q + q0 + qi) * p.H + h) * p.D + c;
-            if ((p.D % kVec) == 0 && (reinterpret_cast<uintptr_t>(gout) & 15) == 0) {
-              *reinterpret_cast<uint4*>(wtile + e) = *reinterpret_cast<const uint4*>(src);
-            } else {
-              for (int v = 0; v < kVec && e + v < qn * p.D; ++v) {
-                const int qv = (e + v) / p.D, cv = (e + v) - qv * p.D;
-                wtile[e + v] = gout[((int64_t(b) * p.Q + q0 + qv) * p.H + h) * p.D + cv];
-              }
+          const LocPair<TL> lp = sloc[tid];
+          A a = to_acc(sattn[tid]);
+          if (!tile_vec) {
+            for (int e = lane; e < qn * p.D; e += kWave) {
+              const int qi = e / p.D, c = e - qi * p.D;
+              wtile[e] = gout[((int64_t(b) * p.Q + q0 + qi) * p.H + h) * p.D + c];
             }
           }
-          if constexpr (SOFTMAX) {
+        if constexpr (SOFTMAX) {
             // The P2 lanes of a query share its L * P logits: max, then sum of exp.
             const T* ua = attn_all + unit * LP;
             A mx = -INFINITY;
@@ -738,7 +822,7 @@ __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
             if (bs.ok) a = exp_acc(load_acc(ua + s) - mx) / sum;
           }
           if (bs.ok) {
-            const Geom<A> g = geometry<A>(lx, ly, lv, 0u, 1u);
+            const Geom<A> g = geometry<A>(to_acc(lp.x), to_acc(lp.y), lv, 0u, 1u);
             const bool m[4] = {g.m00, g.m01, g.m10, g.m11};
             const A wb[4] = {g.w00, g.w01, g.w10, g.w11};
 #pragma unroll
@@ -753,7 +837,7 @@ __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
 #pragma unroll
         for (int c = 0; c < 4; ++c)
           if (rv[c]) atomicAdd(&cnt[rpos[c]], 1);
-        __syncthreads();
+        lds_barrier();
         // C. Start of every position's run.
         {
           int total;
@@ -765,7 +849,7 @@ __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
           }
           if (tid == 0) start[npos] = total;
         }
-        __syncthreads();
+        lds_barrier();
         // D. Place the records.
         const uint32_t qslot = uint32_t(wave * qb + (lane >> gp.p2_log2));
 #pragma unroll
@@ -775,7 +859,7 @@ __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
             sorted[dst] = SortedRec<A>{rw[c], qslot};
           }
         }
-        __syncthreads();
+        lds_barrier();
         // E. Accumulate the runs of the owned items.
 #pragma unroll
         for (int k = 0; k < kItemsPerThread; ++k) {
@@ -794,7 +878,12 @@ __global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
           }
         }
         for (int i = tid; i < npos; i += nthreads) cnt[i] = 0;
-        __syncthreads();
+        lds_barrier();
+        sloc[tid] = nxt.loc;
+        sattn[tid] = nxt.a;
+        if (tile_vec && lane * kVec < tile) *reinterpret_cast<uint4*>(wtile + lane * kVec) = nxt.tv;
+        cur_has = nxt.has;
+        cur_j = nxt.j;
       }
     }
   }
@@ -1100,7 +1189,9 @@ size_t grad_value_lds(int dtype, int threads, int64_t L, int64_t D, int qb, int6
   at += (es * waves * size_t(qb) * size_t(D) + 15) & ~size_t(15);
   at += sizeof(int) * (3 * size_t(npos) + 1);
   at += sizeof(int) * size_t(threads);
-  at += sizeof(int) * waves;
+  at += (sizeof(int) * waves + 15) & ~size_t(15);
+  at += (dtype == MSDA_F64 ? 16 : 8) * size_t(threads);  // staged location pairs (widest case)
+  at += es * size_t(threads);                            // staged weights
   return at;
 }
 
