@@ -107,10 +107,12 @@ template <typename T, int CV> struct Chan;
 
 template <int CV> struct Chan<float, CV> {
   using R = Raw<4 * CV>;
-  static __device__ inline void load(const char* p, float (&v)[CV]) {
-    const R r = *reinterpret_cast<const R*>(p);
+  static __device__ inline void from_raw(const R& r, float (&v)[CV]) {
 #pragma unroll
     for (int i = 0; i < CV; ++i) v[i] = __uint_as_float(r.w[i]);
+  }
+  static __device__ inline void load(const char* p, float (&v)[CV]) {
+    from_raw(*reinterpret_cast<const R*>(p), v);
   }
   static __device__ inline void store(char* p, const float (&v)[CV]) {
     R r;
@@ -127,11 +129,13 @@ template <int CV> struct Chan<float, CV> {
 
 template <int CV> struct Chan<double, CV> {
   using R = Raw<8 * CV>;
-  static __device__ inline void load(const char* p, double (&v)[CV]) {
-    const R r = *reinterpret_cast<const R*>(p);
+  static __device__ inline void from_raw(const R& r, double (&v)[CV]) {
 #pragma unroll
     for (int i = 0; i < CV; ++i)
       v[i] = __builtin_bit_cast(double, (uint64_t(r.w[2 * i + 1]) << 32) | r.w[2 * i]);
+  }
+  static __device__ inline void load(const char* p, double (&v)[CV]) {
+    from_raw(*reinterpret_cast<const R*>(p), v);
   }
   static __device__ inline void store(char* p, const double (&v)[CV]) {
     R r;
@@ -165,8 +169,7 @@ template <typename T, int CV> struct Chan16 {
       __builtin_amdgcn_global_atomic_fadd_v2f16(reinterpret_cast<f16x2_v*>(p),
                                                 __builtin_bit_cast(f16x2_v, packed));
   }
-  static __device__ inline void load(const char* p, float (&v)[CV]) {
-    const R r = *reinterpret_cast<const R*>(p);
+  static __device__ inline void from_raw(const R& r, float (&v)[CV]) {
     if constexpr (CV == 1) {
       v[0] = lo(r.h);
     } else {
@@ -176,6 +179,9 @@ template <typename T, int CV> struct Chan16 {
         v[2 * i + 1] = hi(r.w[i]);
       }
     }
+  }
+  static __device__ inline void load(const char* p, float (&v)[CV]) {
+    from_raw(*reinterpret_cast<const R*>(p), v);
   }
   static __device__ inline void store(char* p, const float (&v)[CV]) {
     R r;
@@ -283,6 +289,8 @@ template <typename A> struct Geom {
   A dx, dy;
   A w00, w01, w10, w11;  // bilinear weights, zero for corners outside the level
   uint32_t off[4];
+  int ix, iy;            // top-left corner (floor of the pixel coordinates), when in
+  bool in;               // the sample counts: -1 <= pixel < size on both axes
   bool m00, m01, m10, m11;
 };
 
@@ -300,6 +308,9 @@ __device__ inline Geom<A> geometry(A lx, A ly, const Level lv, uint32_t head_byt
   g.dx = in ? x - xf : A(0);
   g.dy = in ? y - yf : A(0);
   const int ix = int(xf), iy = int(yf);
+  g.ix = ix;
+  g.iy = iy;
+  g.in = in;
   const bool mx0 = in && ix >= 0, mx1 = in && ix + 1 < lv.w;
   const bool my0 = in && iy >= 0, my1 = in && iy + 1 < lv.h;
   g.m00 = mx0 && my0;
@@ -440,88 +451,155 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
 // ---------------------------------------------------------------------------
 // Backward.
 //
-// Three kernels on the caller's stream, no atomics to global memory and no buffer
-// beyond the three gradients:
+// grad_value is computed owner-side: every element has exactly one writer, which
+// sums its contributions in fp32 (fp64 for double) registers and stores once, so
+// there are no atomics on grad_value, no zero-fill and no float32 copy. The
+// location and weight gradients are sample-parallel like the forward. Kernels, in
+// stream order:
 //
-//   msda_row_summary_kernel    For every (b, h, l) and block of QB queries (QB * P2
-//                              = 64 sample slots, P2 = P rounded up to a power of
-//                              two), the range of level-l rows its in-bounds
-//                              corners touch. Stored, as scratch, at the start of
-//                              grad_sampling_locations, which is always large enough
-//                              and is written for real only by the third kernel.
-//   msda_grad_value_kernel     Owner-computes grad_value: one 1024-thread workgroup
-//                              per chunk of NPOS positions of one (b, h) keeps the
-//                              chunk's gradient in LDS (fp32; fp64 for double).
-//                              Its 16 waves walk the query blocks of every level
-//                              that meets the chunk, skip blocks whose row range
-//                              misses it, and add a * w_c * grad_out[b, q, h, :] for
-//                              the corners inside the chunk with LDS atomics. The
-//                              chunk is then written once with plain stores: every
-//                              element of grad_value has exactly one writer, so the
-//                              result needs no zero-fill, accumulates in fp32 and
-//                              does not depend on scheduling beyond fp32 rounding.
-//   msda_grad_sample_kernel    Sample-parallel, laid out like the forward: gathers
-//                              the four corners of each sample, forms
-//                              G_c = <grad_out, value_c>, reduces it across the
-//                              unit's lanes and writes grad_loc and grad_attn (the
-//                              softmax Jacobian included). Runs last, so it
-//                              overwrites the row summaries.
-
-// grad_value, owner-computes, with the chunk accumulator in registers.
+//   msda_bucket_kernel<COUNT>  Counting sort of the samples of every (b, h) by the
+//   msda_bucket_scan_kernel    level tile that holds their top-left corner (tiles
+//   msda_bucket_kernel<PLACE>  are described below). Per workgroup the counts are
+//                              aggregated with LDS integer atomics and published with
+//                              one global atomic per touched bucket; the scan turns
+//                              counts into offsets; the place pass writes every
+//                              in-range sample's index into its bucket. The bucket
+//                              offsets live in grad_attention_weights and the sample
+//                              indices in grad_sampling_locations, both overwritten
+//                              later by msda_grad_sample_kernel, so the backward
+//                              needs no memory beyond its outputs.
+//   msda_gap_zero_kernel       Zeroes grad_value at positions no valid level covers.
+//   msda_grad_value_kernel     One tile per workgroup (loop): reads the buckets that
+//                              can reach the tile, stages their grad_out rows in
+//                              LDS, sorts their corner records by position (LDS
+//                              integer counting sort) and accumulates
+//                              weight * grad_out into registers owned per
+//                              (position, channel group). Then one plain store per
+//                              element.
+//   msda_grad_sample_kernel    Location and weight gradients, sample-parallel.
 //
-// Workgroup (b, h, chunk) owns NPOS consecutive positions of grad_value[b, :, h, :].
-// Thread t owns the "items" t, t + T, t + 2T, t + 3T (T threads): item i is position
-// i / G and channel group i % G (G = D / CVR groups of CVR channels), so the whole
-// chunk lives in fp32 (fp64) registers. Per batch of up to one query block per
-// wave:
-//   A. each wave stages its block's grad_out vectors in LDS and turns every sample
-//      of the block into up to four corner records (position in the chunk, query
-//      slot, attention * bilinear weight) kept in registers;
-//   B. a histogram of the records per position (LDS integer atomics);
-//   C. an exclusive scan of the histogram (the start of each position's run);
-//   D. each record claims a slot in its position's run (integer atomic) and is
-//      stored there;
-//   E. each thread walks the runs of the positions it owns and accumulates
-//      weight * grad_out into its registers with plain FMAs.
-// No floating-point atomics are used: on gfx950 the LDS ones retire at a fraction
-// of a lane per clock, while integer LDS atomics run near LDS store rate. Query
-// blocks whose row range misses the chunk are never loaded.
+// Tiles. Level l is cut into rectangles of th x tw positions (at most `cap`, the
+// positions one workgroup holds in registers). The target area follows the level's
+// expected fan-in (4 Q P corner records spread over h * w positions) so that tiles
+// carry similar numbers of records; it is never below `amin`, so a level has at most
+// 3 h w / amin + 1 tiles. A sample is filed under the tile of its top-left corner
+// (clamped to 0) with a sub-bucket that says whether its corners reach into the
+// right-hand tile (1), the tile below (3), both (2) or neither (0). The owner of a
+// tile reads its own four sub-buckets, sub-buckets 1-2 of its left neighbour, 2-3 of
+// the tile above and 2 of the tile above-left: exactly the samples with a corner in
+// the tile.
+//
+// When the scratch cannot hold the bucket offsets (few samples and many tiles) the
+// bucketing is skipped and every tile owner scans all Q * P samples of its level
+// instead; both paths give the same result.
 
-constexpr int kGradValueMaxThreads = 1024;
-constexpr int kItemsPerThread = 4;
-constexpr int kRecordsPerWave = 4 * kWave;
+constexpr int kOwnerThreads = 256;
+constexpr int kOwnerItems = 4;      // (position, channel group) items per thread
+constexpr int kOwnerChunks = 4;     // grad_out pieces one thread stages per batch
+constexpr int kBucketThreads = 256;
+constexpr int kBucketSamples = 32;  // samples per thread in the bucketing kernels
+constexpr int kBucketBatch = 8;     // of which loaded together
+constexpr int kTargetRecords = 8192;
+constexpr int kBucketLdsKeys = 8192;  // LDS bucket counters of the bucketing kernels (32 KB)
+constexpr int kMaxOrderedLevels = 64;
 
-struct GradValuePlan {
-  int npos;       // positions per chunk
-  int nchunks;    // chunks per (b, h)
-  int p2_log2;    // log2 of P rounded up to a power of two
-  int nblocks;    // query blocks per (b, h, l): ceil(Q / QB), QB = 64 >> p2_log2
-  int groups;     // channel groups per position, G = D / CVR
+// Unsigned 32-bit division by a divisor fixed per launch: one multiply-high, an
+// add and two shifts (Granlund and Montgomery, "Division by invariant integers
+// using multiplication", 1994, section 4) instead of the ~30-instruction software
+// division. Exact for every dividend below 2^32.
+struct FastDiv {
+  uint32_t d, m;
+  int s;
 };
 
-struct alignas(8) RowRange {
-  int lo, hi;
+FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f{d, 0u, 0};
+  if (d <= 1) return f;
+  int l = 0;
+  while ((uint64_t(1) << l) < d) ++l;  // ceil(log2 d)
+  f.m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+  f.s = l - 1;
+  return f;
+}
+
+__device__ inline uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  if (f.d <= 1) return n;
+  const uint32_t t = __umulhi(f.m, n);
+  return (t + ((n - t) >> 1)) >> f.s;
+}
+
+struct BwdGeom {
+  int cap;          // positions per tile at most (power of two)
+  int amin;         // smallest tile area (power of two)
+  int groups;       // G = D / CVR channel groups per position
+  int nb;           // samples per owner batch (power of two, <= kOwnerThreads)
+  int nw;           // owner workgroups per (b, h)
+  int keys_lds;     // bucket counters the bucketing kernels' LDS holds
+  int64_t keys_alloc;  // bucket counters per (b, h) the scratch holds; 0: no bucketing
+  int64_t region;   // entries per (b, h): Q * L * P
+  FastDiv div_lp;   // by L * P
+  FastDiv div_p;    // by P
 };
 
-template <typename A> struct alignas(8) SortedRec {
-  A w;
-  uint32_t qslot;  // wave * QB + query in block
+struct LevelTiles {
+  int lh, lw;     // log2 of the tile height and width
+  int ntx, nty;   // tiles across and down
+  int base;       // first tile of the level
 };
 
-// The normalized weight of sample s of a unit: the raw weight, or its softmax over
-// the unit's L * P logits (max first, so -inf logits are safe).
-template <typename T, bool SOFTMAX>
-__device__ inline typename Elem<T>::acc unit_weight(const T* unit_attn, int LP, int s) {
-  using A = typename Elem<T>::acc;
-  if constexpr (!SOFTMAX) {
-    return load_acc(unit_attn + s);
-  } else {
-    A mx = -INFINITY;
-    for (int i = 0; i < LP; ++i) mx = fmax(mx, load_acc(unit_attn + i));
-    A sum(0);
-    for (int i = 0; i < LP; ++i) sum += exp_acc(load_acc(unit_attn + i) - mx);
-    return exp_acc(load_acc(unit_attn + s) - mx) / sum;
+__device__ __host__ inline int pow2_floor(int64_t v) {
+  int r = 1;
+  while (int64_t(r) * 2 <= v && r < (1 << 30)) r *= 2;
+  return r;
+}
+
+__device__ inline int log2_ceil(int v) {
+  int r = 0;
+  while ((1 << r) < v && r < 30) ++r;
+  return r;
+}
+
+// Tiles of every level (one thread). Tile sides are powers of two, so that tiles
+// and sub-buckets follow from shifts and masks; a tile may reach past the level's
+// right or bottom edge. Returns the tile count of one (b, h), or -1 when it exceeds
+// 2^29.
+__device__ inline int64_t plan_tiles(const Problem& p, const BwdGeom& bg, const Level* levels,
+                                     LevelTiles* lt) {
+  int64_t total = 0;
+  const int64_t records = 4 * int64_t(p.Q) * p.P;
+  for (int l = 0; l < p.L; ++l) {
+    const Level lv = levels[l];
+    LevelTiles t{0, 0, 0, 0, int(total)};
+    if (lv.ok) {
+      const int64_t hw = int64_t(lv.h) * lv.w;
+      const int64_t want = records > 0 ? int64_t(kTargetRecords) * hw / records : bg.cap;
+      const int a = pow2_floor(std::min<int64_t>(std::max<int64_t>(want, bg.amin), bg.cap));
+      int tw0 = 1;
+      while (tw0 * tw0 < a) tw0 *= 2;
+      const int wcap = 1 << log2_ceil(lv.w), hcap = 1 << log2_ceil(lv.h);
+      int tw = min(wcap, tw0);
+      const int th = min(hcap, max(1, a / tw));
+      tw = min(wcap, max(tw, a / th));
+      t.lw = log2_ceil(tw);
+      t.lh = log2_ceil(th);
+      t.ntx = (lv.w + tw - 1) >> t.lw;
+      t.nty = (lv.h + th - 1) >> t.lh;
+    }
+    lt[l] = t;
+    total += int64_t(t.ntx) * t.nty;
+    if (total > (int64_t(1) << 29)) return -1;
   }
+  return total;
+}
+
+// The bucket key of an in-range sample at level l: 4 * tile + sub-bucket.
+__device__ inline int bucket_key(const LevelTiles& t, int ix, int iy, const Level& lv) {
+  const int cx = max(ix, 0), cy = max(iy, 0);
+  const int tile = t.base + (cy >> t.lh) * t.ntx + (cx >> t.lw);
+  const bool sx = ix >= 0 && ix + 1 < lv.w && ((ix + 1) & ((1 << t.lw) - 1)) == 0;
+  const bool sy = iy >= 0 && iy + 1 < lv.h && ((iy + 1) & ((1 << t.lh) - 1)) == 0;
+  const int sub = sx ? (sy ? 2 : 1) : (sy ? 3 : 0);
+  return 4 * tile + sub;
 }
 
 // Workgroup barrier for LDS traffic only: the fences are restricted to the local
@@ -564,68 +642,178 @@ __device__ inline int block_exclusive_scan(int v, int* wave_sums, int* total) {
   return before + inc - v;
 }
 
-// The sample of lane `lane` in block j: (query, point), and whether it exists.
-struct BlockSlot {
-  int q, pt;
-  bool ok;
-};
-__device__ inline BlockSlot block_slot(const Problem& p, int p2_log2, int j, int lane) {
-  BlockSlot bs;
-  bs.q = (j << (6 - p2_log2)) + (lane >> p2_log2);
-  bs.pt = lane & ((1 << p2_log2) - 1);
-  bs.ok = bs.q < p.Q && bs.pt < p.P;
-  return bs;
+// The normalized weight of sample s of a unit: the raw weight, or its softmax over
+// the unit's L * P logits (max first, so -inf logits are safe).
+template <typename T, bool SOFTMAX>
+__device__ inline typename Elem<T>::acc unit_weight(const T* unit_attn, int LP, int s) {
+  using A = typename Elem<T>::acc;
+  if constexpr (!SOFTMAX) {
+    return load_acc(unit_attn + s);
+  } else {
+    A mx = -INFINITY;
+    for (int i = 0; i < LP; ++i) mx = fmax(mx, load_acc(unit_attn + i));
+    A sum(0);
+    for (int i = 0; i < LP; ++i) sum += exp_acc(load_acc(unit_attn + i) - mx);
+    return exp_acc(load_acc(unit_attn + s) - mx) / sum;
+  }
 }
 
-// One wave per (b, h, l, block): the range of level-l rows the block's in-bounds
-// corners touch (lo > hi when none). Same geometry code and precision as the
-// grad_value kernel, so both place every corner in the same row.
-template <typename T, typename TL>
-__global__ __launch_bounds__(256) void msda_row_summary_kernel(const Problem p, const GradValuePlan gp,
-                                                               RowRange* __restrict__ out) {
-  using A = typename Elem<T>::acc;
-  const int64_t entries = int64_t(p.B) * p.H * p.L * gp.nblocks;
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t e = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) / kWave;
-  if (e >= entries) return;  // uniform per wave
-  const int j = int(e % gp.nblocks);
-  const int l = int((e / gp.nblocks) % p.L);
-  const int h = int((e / (int64_t(gp.nblocks) * p.L)) % p.H);
-  const int b = int(e / (int64_t(gp.nblocks) * p.L * p.H));
-  int64_t hh, ww, st;
-  if (p.index_i32) {
-    hh = static_cast<const int32_t*>(p.shapes)[2 * l];
-    ww = static_cast<const int32_t*>(p.shapes)[2 * l + 1];
-    st = static_cast<const int32_t*>(p.starts)[l];
-  } else {
-    hh = static_cast<const int64_t*>(p.shapes)[2 * l];
-    ww = static_cast<const int64_t*>(p.shapes)[2 * l + 1];
-    st = static_cast<const int64_t*>(p.starts)[l];
-  }
-  const bool ok = hh > 0 && ww > 0 && st >= 0 && hh <= p.S && ww <= p.S && st + hh * ww <= p.S;
-  const Level lv = ok ? Level{int(hh), int(ww), int(st), 1} : Level{1, 1, 0, 0};
-  const BlockSlot bs = block_slot(p, gp.p2_log2, j, lane);
-  int lo = INT32_MAX, hi = INT32_MIN;
-  if (bs.ok) {
-    const int LP = p.L * p.P;
-    const int64_t unit = (int64_t(b) * p.Q + bs.q) * p.H + h;
-    const TL* lc = reinterpret_cast<const TL*>(p.loc) + (unit * LP + l * p.P + bs.pt) * 2;
+// Shared set-up of the bucketing kernels and the owner: the level table and the
+// tiles in LDS. Returns the tile count of one (b, h) (-1: too many).
+__device__ inline int64_t load_tiles(const Problem& p, const BwdGeom& bg, Level* levels,
+                                     LevelTiles* lt, int64_t* total_out) {
+  load_levels(p, levels);
+  __syncthreads();
+  if (threadIdx.x == 0) *total_out = plan_tiles(p, bg, levels, lt);
+  __syncthreads();
+  return *total_out;
+}
+
+// Counting (PLACE = false) or placing (PLACE = true) pass of the bucket sort.
+// Workgroup: kBucketThreads * kBucketSamples consecutive samples (q, l, p) of one
+// (b, h). `buckets` holds one counter per bucket and (b, h): counts after the count
+// pass, exclusive offsets after the scan, and bucket ends after the place pass.
+// The workgroup first counts its samples per bucket in LDS and publishes each
+// non-empty count with one global atomic; the place pass gets its range of every
+// bucket back from that atomic and hands out slots from it with LDS atomics while
+// it recomputes the keys.
+template <typename TL, bool PLACE>
+__global__ __launch_bounds__(kBucketThreads) void msda_bucket_kernel(const Problem p, const BwdGeom bg,
+                                                                     int* __restrict__ buckets,
+                                                                     uint32_t* __restrict__ entries,
+                                                                     int chunks_per_bh) {
+  using A = typename Elem<TL>::acc;  // the precision the owner kernel's geometry uses
+  extern __shared__ __align__(16) unsigned char smem[];
+  Level* levels = reinterpret_cast<Level*>(smem);
+  LevelTiles* lt = reinterpret_cast<LevelTiles*>(smem + sizeof(Level) * size_t(p.L));
+  const size_t head = ((sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) + 15) & ~size_t(15);
+  int64_t* total = reinterpret_cast<int64_t*>(smem + head);
+  int* hist = reinterpret_cast<int*>(smem + head + 16);
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
+  const int64_t nkeys = 4 * ntiles;
+  if (ntiles < 0 || nkeys > bg.keys_alloc) return;  // no bucketing: the owners scan
+  const bool in_lds = nkeys <= bg.keys_lds;
+  const int bh = int(blockIdx.x) / chunks_per_bh;
+  const int chunk = int(blockIdx.x) - bh * chunks_per_bh;
+  const int b = bh / p.H, h = bh - b * p.H;
+  const int LP = p.L * p.P;
+  const int64_t nsamples = int64_t(p.Q) * LP;
+  int* bucket_row = buckets + int64_t(bh) * nkeys;
+  uint32_t* out = entries + int64_t(bh) * bg.region;
+  const TL* loc_all = reinterpret_cast<const TL*>(p.loc);
+  const int64_t j0 = int64_t(chunk) * kBucketThreads * kBucketSamples;
+
+  // Bucket of sample j of (b, h), or -1 when it is out of range (or j past the end).
+  auto key_of = [&](int64_t j) __attribute__((always_inline)) -> int {
+    if (j >= nsamples) return -1;
+    const uint32_t j32 = uint32_t(j);  // Q * L * P < 2^32
+    const int q = int(fdiv(j32, bg.div_lp)), s = int(j32 - uint32_t(q) * uint32_t(LP));
+    const int l = int(fdiv(uint32_t(s), bg.div_p));
+    const Level lv = levels[l];
+    const TL* lc = loc_all + (((int64_t(b) * p.Q + q) * p.H + h) * LP + s) * 2;
     const Geom<A> g = geometry<A>(load_acc(lc), load_acc(lc + 1), lv, 0u, 1u);
-    if (g.m00 || g.m01) lo = hi = (int(g.off[g.m00 ? 0 : 1]) - lv.start) / lv.w;
-    if (g.m10 || g.m11) {
-      const int r = (int(g.off[g.m10 ? 2 : 3]) - lv.start) / lv.w;
-      lo = min(lo, r);
-      hi = max(hi, r);
+    return g.in ? bucket_key(lt[l], g.ix, g.iy, lv) : -1;
+  };
+
+  if (!in_lds) {
+    // Too many buckets for LDS: one global atomic per sample.
+    for (int k = 0; k < kBucketSamples; k += kBucketBatch) {
+      int key[kBucketBatch];
+#pragma unroll
+      for (int i = 0; i < kBucketBatch; ++i) key[i] = key_of(j0 + (k + i) * kBucketThreads + threadIdx.x);
+#pragma unroll
+      for (int i = 0; i < kBucketBatch; ++i) {
+        if (key[i] < 0) continue;
+        const int at = atomicAdd(&bucket_row[key[i]], 1);
+        if constexpr (PLACE) out[at] = uint32_t(j0 + (k + i) * kBucketThreads + threadIdx.x);
+      }
+    }
+    return;
+  }
+  for (int k = threadIdx.x; k < nkeys; k += kBucketThreads) hist[k] = 0;
+  __syncthreads();
+  for (int k = 0; k < kBucketSamples; k += kBucketBatch) {
+    int key[kBucketBatch];
+#pragma unroll
+    for (int i = 0; i < kBucketBatch; ++i) key[i] = key_of(j0 + (k + i) * kBucketThreads + threadIdx.x);
+#pragma unroll
+    for (int i = 0; i < kBucketBatch; ++i)
+      if (key[i] >= 0) atomicAdd(&hist[key[i]], 1);
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < nkeys; k += kBucketThreads) {
+    const int c = hist[k];
+    if (c > 0) {
+      const int at = atomicAdd(&bucket_row[k], c);
+      if constexpr (PLACE) hist[k] = at;  // becomes this workgroup's cursor in bucket k
     }
   }
-  for (int m = 1; m < kWave; m <<= 1) {
-    lo = min(lo, __shfl_xor(lo, m, kWave));
-    hi = max(hi, __shfl_xor(hi, m, kWave));
+  if constexpr (PLACE) {
+    __syncthreads();
+    for (int k = 0; k < kBucketSamples; k += kBucketBatch) {
+      int key[kBucketBatch];
+#pragma unroll
+      for (int i = 0; i < kBucketBatch; ++i) key[i] = key_of(j0 + (k + i) * kBucketThreads + threadIdx.x);
+#pragma unroll
+      for (int i = 0; i < kBucketBatch; ++i)
+        if (key[i] >= 0) out[atomicAdd(&hist[key[i]], 1)] = uint32_t(j0 + (k + i) * kBucketThreads + threadIdx.x);
+    }
   }
-  if (lane == 0) out[e] = RowRange{lo, hi};
 }
 
-// Raw (unconverted) element types, so that a prefetch does not wait for its data.
+// Counts to exclusive offsets, one workgroup per (b, h).
+__global__ __launch_bounds__(1024) void msda_bucket_scan_kernel(const Problem p, const BwdGeom bg,
+                                                                int* __restrict__ buckets) {
+  __shared__ Level levels_s[kMaxOrderedLevels];
+  __shared__ LevelTiles lt_s[kMaxOrderedLevels];
+  __shared__ int64_t total_s[2];
+  __shared__ int wave_sums[1024 / kWave];
+  extern __shared__ __align__(16) unsigned char smem[];
+  Level* levels = p.L <= kMaxOrderedLevels ? levels_s : reinterpret_cast<Level*>(smem);
+  LevelTiles* lt = p.L <= kMaxOrderedLevels ? lt_s
+                                             : reinterpret_cast<LevelTiles*>(smem + sizeof(Level) * size_t(p.L));
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total_s);
+  const int64_t nkeys = 4 * ntiles;
+  if (ntiles < 0 || nkeys > bg.keys_alloc) return;
+  int* row = buckets + int64_t(blockIdx.x) * nkeys;
+  int carry = 0;
+  for (int64_t k0 = 0; k0 < nkeys; k0 += blockDim.x) {
+    const int64_t k = k0 + threadIdx.x;
+    const int v = k < nkeys ? row[k] : 0;
+    int sum;
+    const int ex = block_exclusive_scan(v, wave_sums, &sum);
+    if (k < nkeys) row[k] = carry + ex;
+    carry += sum;
+  }
+}
+
+// Zeroes grad_value[b, pos, :, :] at every position no valid level covers; the tile
+// owners write all the others.
+template <typename T>
+__global__ __launch_bounds__(256) void msda_gap_zero_kernel(const Problem p) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  Level* levels = reinterpret_cast<Level*>(smem);
+  load_levels(p, levels);
+  __syncthreads();
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= int64_t(p.B) * p.S) return;
+  const int pos = int(idx % p.S);
+  bool covered = false;
+  for (int l = 0; l < p.L && !covered; ++l) {
+    const Level lv = levels[l];
+    covered = lv.ok && pos >= lv.start && int64_t(pos) < int64_t(lv.start) + int64_t(lv.h) * lv.w;
+  }
+  if (covered) return;
+  T* dst = reinterpret_cast<T*>(p.grad_value) + idx * p.H * p.D;
+  for (int i = 0; i < p.H * p.D; ++i) store_elem(dst + i, typename Elem<T>::acc(0));
+}
+
+template <typename A> struct alignas(8) TileRec {
+  A w;
+  uint32_t slot;
+};
+
+// Raw (unconverted) loads for the prefetch, so that it does not wait for its data.
 __device__ inline float to_acc(float v) { return v; }
 __device__ inline double to_acc(double v) { return v; }
 __device__ inline float to_acc(bf16_t v) { return __uint_as_float(uint32_t(v.bits) << 16); }
@@ -635,275 +823,334 @@ template <typename TL> struct LocPair {
   TL x, y;
 };
 
-// Register copy of what one wave needs from global memory for one query block:
-// the lane's location pair and weight, and one 16-byte piece of the block's
-// grad_out tile. Kept raw and converted at use, so the loads of the next block stay
-// in flight while the current one is processed.
-template <typename T, typename TL> struct BlockFetch {
-  bool has;
-  int j;
-  LocPair<TL> loc;
-  T a;
-  uint4 tv;
+// One grad_out piece of CVR channels as a native vector type, so that arrays of
+// them stay in VGPRs across the batch loop.
+typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
+template <int BYTES> struct PieceOf;
+template <> struct PieceOf<2> { using type = uint16_t; };
+template <> struct PieceOf<4> { using type = uint32_t; };
+template <> struct PieceOf<8> { using type = u32x2_v; };
+template <> struct PieceOf<16> { using type = u32x4_v; };
+template <typename T, int CVR> using Piece = typename PieceOf<Elem<T>::size * CVR>::type;
+
+// grad_out rows are staged in LDS in the accumulation type, CVR values per piece.
+template <typename A, int CVR> struct alignas(CVR * sizeof(A) < 16 ? CVR * sizeof(A) : 16) AccPiece {
+  A v[CVR];
 };
 
-// Branch-free: every lane issues the same three loads (from clamped, always valid
-// addresses) and selects afterwards, so the compiler can count them and leave them in
-// flight while the previous block is processed.
-template <typename T, typename TL, bool SOFTMAX>
-__device__ inline BlockFetch<T, TL> fetch_block(const Problem& p, const GradValuePlan& gp, int sidx,
-                                                int nsel, const int* blist, int l, int b, int h,
-                                                const TL* loc_all, const T* attn_all, const T* gout,
-                                                bool tile_vec) {
-  constexpr int kVec = 16 / Elem<T>::size;
-  const int lane = threadIdx.x & (kWave - 1);
-  BlockFetch<T, TL> f;
-  f.has = sidx < nsel;
-  // blist[0] is a block of this round only when nsel > 0; otherwise read block 0,
-  // which exists whenever the kernel runs (Q > 0). Clamped, so every address below
-  // stays inside the tensors whatever the LDS holds.
-  const int jj = f.has ? blist[sidx] : (nsel > 0 ? blist[0] : 0);
-  f.j = min(max(jj, 0), gp.nblocks - 1);
-  const int qb = kWave >> gp.p2_log2;
-  const int q0 = f.j * qb;
-  const int qn = min(qb, p.Q - q0);
-  const BlockSlot bs = block_slot(p, gp.p2_log2, f.j, lane);
-  const int LP = p.L * p.P;
-  const int q = bs.ok ? bs.q : q0;
-  const int s = l * p.P + (bs.ok ? bs.pt : 0);
-  const int64_t unit = (int64_t(b) * p.Q + q) * p.H + h;
-  f.loc = *reinterpret_cast<const LocPair<TL>*>(loc_all + (unit * LP + s) * 2);
-  if constexpr (!SOFTMAX) f.a = attn_all[unit * LP + s];
-  else f.a = T{};
-  int e = lane * kVec;
-  if (!(tile_vec && e < qn * p.D)) e = 0;
-  const int qi = e / p.D, c = e - qi * p.D;
-  if (tile_vec)
-    f.tv = *reinterpret_cast<const uint4*>(gout + ((int64_t(b) * p.Q + q0 + qi) * p.H + h) * p.D + c);
-  else
-    f.tv = make_uint4(0, 0, 0, 0);
-  return f;
-}
-
+// Owner-computes grad_value. Workgroup (slot, b, h) takes tiles slot, slot + nw, ...
+// of (b, h) in descending order of expected records per tile. For each tile, batches
+// of nb candidate samples:
+//   A. thread t < nb turns candidate t into up to four corner records (position in
+//      the tile, its sample slot, attention * bilinear weight) and ranks each record
+//      within its position with an LDS integer atomic on the histogram;
+//   B. an exclusive scan of the histogram gives each position's run;
+//   C. records move to run start + rank;
+//   D. each thread walks the runs of the (position, channel group) items it owns
+//      and accumulates weight * grad_out, four records at a time, from grad_out
+//      rows staged in LDS (converted to the accumulation type once, when staged).
+// Software pipeline: the sample index of every candidate of the next batch sits in
+// LDS (`qnext`); at the top of a batch each thread loads its next sample's location
+// and weight and its share of the next batch's grad_out rows, and the index of its
+// sample two batches ahead; these arrive while the batch is processed and move to
+// LDS / registers after it.
 template <typename T, typename TL, int CVR, bool SOFTMAX>
-__global__ __launch_bounds__(kGradValueMaxThreads) void msda_grad_value_kernel(
-    const Problem p, const GradValuePlan gp, const RowRange* __restrict__ rows, const int accumulate) {
+__global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
+    const Problem p, const BwdGeom bg, const int* __restrict__ buckets,
+    const uint32_t* __restrict__ entries, const int accumulate) {
   using A = typename Elem<T>::acc;
+  using PieceT = Piece<T, CVR>;
+  using Raw_ = Raw<Elem<T>::size * CVR>;
+  using APiece = AccPiece<A, CVR>;
   constexpr int ES = Elem<T>::size;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int nthreads = int(blockDim.x), nwaves = nthreads / kWave;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
-  const int qb = kWave >> gp.p2_log2;
-  const int npos = gp.npos;
+  const int tid = threadIdx.x;
+  const int G = bg.groups, nb = bg.nb, cap = bg.cap;
+  const int LP = p.L * p.P;
+  const size_t rstride = size_t(p.D) * sizeof(A) + 16;  // padded: fewer bank conflicts
 
   // LDS layout; every offset is an integer added to smem, so accesses stay ds_*.
   size_t at = 0;
   Level* levels = reinterpret_cast<Level*>(smem + at);
   at += sizeof(Level) * size_t(p.L);
-  SortedRec<A>* sorted = reinterpret_cast<SortedRec<A>*>(smem + at);
-  at += sizeof(SortedRec<A>) * size_t(nwaves) * kRecordsPerWave;
-  T* gtile = reinterpret_cast<T*>(smem + at);
-  at += (sizeof(T) * size_t(nwaves) * qb * p.D + 15) & ~size_t(15);
+  LevelTiles* lt = reinterpret_cast<LevelTiles*>(smem + at);
+  at += sizeof(LevelTiles) * size_t(p.L);
+  int* order = reinterpret_cast<int*>(smem + at);  // levels, heaviest tiles first
+  at += sizeof(int) * size_t(p.L);
+  int* rank_base = reinterpret_cast<int*>(smem + at);  // first tile rank per ordered level
+  at += sizeof(int) * size_t(p.L + 1);
+  at = (at + 15) & ~size_t(15);
+  int64_t* total = reinterpret_cast<int64_t*>(smem + at);
+  at += 16;
+  char* gtile = reinterpret_cast<char*>(smem + at);  // nb staged grad_out rows
+  at += size_t(nb) * rstride;
+  TileRec<A>* recs = reinterpret_cast<TileRec<A>*>(smem + at);
+  at += sizeof(TileRec<A>) * size_t(4 * nb);
+  uint32_t* qnext = reinterpret_cast<uint32_t*>(smem + at);  // next batch's sample indices
+  at += sizeof(uint32_t) * size_t(nb);
   int* cnt = reinterpret_cast<int*>(smem + at);
-  at += sizeof(int) * size_t(npos);
-  int* start = reinterpret_cast<int*>(smem + at);  // npos + 1 entries
-  at += sizeof(int) * size_t(npos + 1);
-  int* cursor = reinterpret_cast<int*>(smem + at);
-  at += sizeof(int) * size_t(npos);
-  int* blist = reinterpret_cast<int*>(smem + at);  // selected blocks, one per thread
-  at += sizeof(int) * size_t(nthreads);
+  at += sizeof(int) * size_t(cap);
+  int* start = reinterpret_cast<int*>(smem + at);  // cap + 1 entries
+  at += sizeof(int) * size_t(cap + 1);
   int* wave_sums = reinterpret_cast<int*>(smem + at);
-  at += (sizeof(int) * size_t(nwaves) + 15) & ~size_t(15);
-  LocPair<TL>* sloc = reinterpret_cast<LocPair<TL>*>(smem + at);  // per lane: the staged location
-  at += sizeof(LocPair<TL>) * size_t(nthreads);
-  T* sattn = reinterpret_cast<T*>(smem + at);  // per lane: the staged weight
 
-  const int n = int(gridDim.x), per = n / kXcds, rem = n % kXcds;
-  const int xcd = int(blockIdx.x) % kXcds, slot = int(blockIdx.x) / kXcds;
-  const int blk = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
-  // Last chunks first: with pyramids stored fine to coarse they hold the coarse,
-  // most sampled levels, so the longest workgroups start earliest.
-  const int chunk = gp.nchunks - 1 - blk % gp.nchunks;
-  const int bh = blk / gp.nchunks;
-  const int h = bh % p.H, b = bh / p.H;
-  const int p0 = chunk * npos;
-  const int p1 = min(p0 + npos, p.S);
-  const int LP = p.L * p.P;
-
-  load_levels(p, levels);
-  for (int i = tid; i < npos; i += nthreads) cnt[i] = 0;
-
-  A accum[kItemsPerThread][CVR];
-#pragma unroll
-  for (int k = 0; k < kItemsPerThread; ++k)
-#pragma unroll
-    for (int c = 0; c < CVR; ++c) accum[k][c] = A(0);
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
+  if (ntiles <= 0) return;
+  const bool bucketed = 4 * ntiles <= bg.keys_alloc;
+  if (tid == 0) {
+    // Order the levels by expected records per tile (tile area / level area),
+    // heaviest first, so the longest workgroups start first.
+    for (int i = 0; i < p.L; ++i) order[i] = i;
+    if (p.L <= kMaxOrderedLevels) {
+      for (int i = 0; i < p.L; ++i) {
+        int best = i;
+        for (int k = i + 1; k < p.L; ++k) {
+          const int a = order[k], c = order[best];
+          const int64_t ha = int64_t(levels[a].h) * levels[a].w, hc = int64_t(levels[c].h) * levels[c].w;
+          const int64_t ta = int64_t(1) << (lt[a].lh + lt[a].lw), tc = int64_t(1) << (lt[c].lh + lt[c].lw);
+          if (ta * hc > tc * ha) best = k;
+        }
+        const int tmp = order[i];
+        order[i] = order[best];
+        order[best] = tmp;
+      }
+    }
+    int acc_tiles = 0;
+    for (int i = 0; i < p.L; ++i) {
+      rank_base[i] = acc_tiles;
+      acc_tiles += lt[order[i]].ntx * lt[order[i]].nty;
+    }
+    rank_base[p.L] = acc_tiles;
+    for (int i = 0; i < cap; ++i) cnt[i] = 0;
+  }
   __syncthreads();
 
+  const int nbh = p.B * p.H;
+  const int slot0 = int(blockIdx.x) / nbh;
+  const int bh = int(blockIdx.x) - slot0 * nbh;
+  const int b = bh / p.H, h = bh - b * p.H;
   const T* gout = reinterpret_cast<const T*>(p.grad_out);
   const T* attn_all = reinterpret_cast<const T*>(p.attn);
   const TL* loc_all = reinterpret_cast<const TL*>(p.loc);
-  const int P2 = 1 << gp.p2_log2;
-  const int tile = qb * p.D;  // elements of one block's grad_out tile
-  constexpr int kVec = 16 / ES;
-  const bool tile_vec = (p.D % kVec) == 0 && (reinterpret_cast<uintptr_t>(gout) & 15) == 0 &&
-                        tile <= kWave * kVec;
+  const uint32_t* ent = entries + int64_t(bh) * bg.region;
+  const int* brow = buckets + int64_t(bh) * 4 * ntiles;
+  const int64_t unit0 = int64_t(b) * p.Q * p.H + h;  // (b, q = 0, h)
 
-  for (int l = 0; l < p.L; ++l) {
-    const Level lv = levels[l];
-    if (!lv.ok) continue;
-    const int a0 = max(p0, lv.start), a1 = min(p1, lv.start + lv.h * lv.w);
-    if (a0 >= a1) continue;  // uniform across the workgroup
-    const int row_lo = (a0 - lv.start) / lv.w, row_hi = (a1 - 1 - lv.start) / lv.w;
-    const RowRange* lrows = rows + ((int64_t(b) * p.H + h) * p.L + l) * gp.nblocks;
-    for (int jb = 0; jb < gp.nblocks; jb += nthreads) {
-      // Select the blocks of this round whose rows reach the chunk.
-      bool reach = false;
-      if (jb + tid < gp.nblocks) {
-        const RowRange rr = lrows[jb + tid];
-        reach = rr.hi >= row_lo && rr.lo <= row_hi;
-      }
-      int nsel;
-      const int at_sel = block_exclusive_scan(reach ? 1 : 0, wave_sums, &nsel);
-      if (reach) blist[at_sel] = jb + tid;
-      lds_barrier();
-      if (nsel == 0) continue;  // uniform across the workgroup
-      // Each wave's current block lives in LDS: its lanes' location pairs and
-      // weights, and the block's grad_out tile. The next block's global loads are
-      // issued at the start of a batch and written to LDS only after the batch's
-      // last barrier, so they stay in flight while the batch is processed.
-      bool cur_has;
-      int cur_j;
-      {
-        const BlockFetch<T, TL> first = fetch_block<T, TL, SOFTMAX>(p, gp, wave, nsel, blist, l, b, h,
-                                                                    loc_all, attn_all, gout, tile_vec);
-        sloc[tid] = first.loc;
-        sattn[tid] = first.a;
-        if (tile_vec && lane * kVec < tile) *reinterpret_cast<uint4*>(gtile + size_t(wave) * tile + lane * kVec) = first.tv;
-        cur_has = first.has;
-        cur_j = first.j;
-      }
-      for (int s0 = 0; s0 < nsel; s0 += nwaves) {
-        const BlockFetch<T, TL> nxt = fetch_block<T, TL, SOFTMAX>(p, gp, s0 + nwaves + wave, nsel, blist,
-                                                                  l, b, h, loc_all, attn_all, gout, tile_vec);
-        // A. One block per wave: records in registers (one slot per corner, so the
-        // arrays stay in VGPRs).
-        bool rv[4] = {false, false, false, false};
-        uint32_t rpos[4] = {0u, 0u, 0u, 0u};
-        A rw[4] = {A(0), A(0), A(0), A(0)};
-        const bool has_block = cur_has;
-        const int j = cur_j;
-        const int q0 = j * qb;
-        const int qn = has_block ? min(qb, p.Q - q0) : 0;
-        T* wtile = gtile + size_t(wave) * tile;
-        if (has_block) {
-          const BlockSlot bs = block_slot(p, gp.p2_log2, j, lane);
-          const int s = l * p.P + bs.pt;
-          const int64_t unit = (int64_t(b) * p.Q + (bs.q < p.Q ? bs.q : q0)) * p.H + h;
-          const LocPair<TL> lp = sloc[tid];
-          A a = to_acc(sattn[tid]);
-          if (!tile_vec) {
-            for (int e = lane; e < qn * p.D; e += kWave) {
-              const int qi = e / p.D, c = e - qi * p.D;
-              wtile[e] = gout[((int64_t(b) * p.Q + q0 + qi) * p.H + h) * p.D + c];
-            }
-          }
-        if constexpr (SOFTMAX) {
-            // The P2 lanes of a query share its L * P logits: max, then sum of exp.
-            const T* ua = attn_all + unit * LP;
-            A mx = -INFINITY;
-            if (bs.q < p.Q)
-              for (int i = bs.pt; i < LP; i += P2) mx = fmax(mx, load_acc(ua + i));
-            for (int m2 = 1; m2 < P2; m2 <<= 1) mx = fmax(mx, __shfl_xor(mx, m2, kWave));
-            A sum(0);
-            if (bs.q < p.Q)
-              for (int i = bs.pt; i < LP; i += P2) sum += exp_acc(load_acc(ua + i) - mx);
-            for (int m2 = 1; m2 < P2; m2 <<= 1) sum += __shfl_xor(sum, m2, kWave);
-            if (bs.ok) a = exp_acc(load_acc(ua + s) - mx) / sum;
-          }
-          if (bs.ok) {
-            const Geom<A> g = geometry<A>(to_acc(lp.x), to_acc(lp.y), lv, 0u, 1u);
-            const bool m[4] = {g.m00, g.m01, g.m10, g.m11};
-            const A wb[4] = {g.w00, g.w01, g.w10, g.w11};
+  // Fixed per thread: the rows and channel groups of its staging pieces, and the
+  // (position, channel group) items it owns.
+  int prow[kOwnerChunks], pgrp[kOwnerChunks], ipos[kOwnerItems], igrp[kOwnerItems];
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              rv[c] = m[c] && int(g.off[c]) >= a0 && int(g.off[c]) < a1;
-              rpos[c] = g.off[c] - uint32_t(p0);
-              rw[c] = wb[c] * a;
-            }
-          }
-        }
-        // B. Histogram.
+  for (int k = 0; k < kOwnerChunks; ++k) {
+    const int u = tid + k * kOwnerThreads;
+    prow[k] = u / G;
+    pgrp[k] = u - prow[k] * G;
+  }
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          if (rv[c]) atomicAdd(&cnt[rpos[c]], 1);
-        lds_barrier();
-        // C. Start of every position's run.
-        {
-          int total;
-          const int v = tid < npos ? cnt[tid] : 0;
-          const int ex = block_exclusive_scan(v, wave_sums, &total);
-          if (tid < npos) {
-            start[tid] = ex;
-            cursor[tid] = ex;
-          }
-          if (tid == 0) start[npos] = total;
-        }
-        lds_barrier();
-        // D. Place the records.
-        const uint32_t qslot = uint32_t(wave * qb + (lane >> gp.p2_log2));
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          if (rv[c]) {
-            const int dst = atomicAdd(&cursor[rpos[c]], 1);
-            sorted[dst] = SortedRec<A>{rw[c], qslot};
-          }
-        }
-        lds_barrier();
-        // E. Accumulate the runs of the owned items.
-#pragma unroll
-        for (int k = 0; k < kItemsPerThread; ++k) {
-          const int item = tid + k * nthreads;
-          const int pos = item / gp.groups, grp = item - pos * gp.groups;
-          if (pos < npos) {
-            const int r1 = start[pos + 1];
-            for (int r = start[pos]; r < r1; ++r) {
-              const SortedRec<A> rec = sorted[r];
-              const T* gq = gtile + size_t(rec.qslot) * p.D + grp * CVR;
-              A gv[CVR];
-              Chan<T, CVR>::load(reinterpret_cast<const char*>(gq), gv);
-#pragma unroll
-              for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec.w, gv[c], accum[k][c]);
-            }
-          }
-        }
-        for (int i = tid; i < npos; i += nthreads) cnt[i] = 0;
-        lds_barrier();
-        sloc[tid] = nxt.loc;
-        sattn[tid] = nxt.a;
-        if (tile_vec && lane * kVec < tile) *reinterpret_cast<uint4*>(wtile + lane * kVec) = nxt.tv;
-        cur_has = nxt.has;
-        cur_j = nxt.j;
-      }
-    }
+  for (int k = 0; k < kOwnerItems; ++k) {
+    const int u = tid + k * kOwnerThreads;
+    ipos[k] = u / G;
+    igrp[k] = u - ipos[k] * G;
   }
 
-  // Write the owned items: the only writer of these grad_value elements.
-  T* gv_out = reinterpret_cast<T*>(p.grad_value);
-  const int64_t img = int64_t(b) * p.S * p.H * p.D;
-#pragma unroll
-  for (int k = 0; k < kItemsPerThread; ++k) {
-    const int item = tid + k * nthreads;
-    const int pos = item / gp.groups, grp = item - pos * gp.groups;
-    if (pos < p1 - p0) {
-      char* dst = reinterpret_cast<char*>(gv_out + img + (int64_t(p0 + pos) * p.H + h) * p.D + grp * CVR);
-      if (accumulate) {
-        A old[CVR];
-        Chan<T, CVR>::load(dst, old);
-#pragma unroll
-        for (int c = 0; c < CVR; ++c) accum[k][c] += old[c];
+  for (int64_t trank = slot0; trank < ntiles; trank += bg.nw) {
+    // The tile: level, rows [r0, r0 + th), columns [c0, c0 + tw), clipped to the level.
+    int oi = 0;
+    while (oi + 1 < p.L && rank_base[oi + 1] <= trank) ++oi;
+    const int l = order[oi];
+    const Level lv = levels[l];
+    const LevelTiles tl = lt[l];
+    const int tile = int(trank) - rank_base[oi];
+    const int ty = tile / tl.ntx, tx = tile - ty * tl.ntx;
+    const int r0 = ty << tl.lh, c0 = tx << tl.lw;
+    const int r1 = min(r0 + (1 << tl.lh), lv.h), c1 = min(c0 + (1 << tl.lw), lv.w);
+    const int npos = 1 << (tl.lh + tl.lw);  // positions past the level's edge stay empty
+
+    // Candidate ranges: the tile's own sub-buckets and its neighbours' straddlers.
+    uint32_t rs[4] = {0u, 0u, 0u, 0u}, rn[4] = {0u, 0u, 0u, 0u};
+    if (bucketed) {
+      auto range = [&](int k_first, int k_last, int i) __attribute__((always_inline)) {
+        const uint32_t s0 = k_first > 0 ? uint32_t(brow[k_first - 1]) : 0u;
+        rs[i] = s0;
+        rn[i] = uint32_t(brow[k_last]) - s0;
+      };
+      const int kt = 4 * (tl.base + tile);
+      range(kt, kt + 3, 0);
+      if (tx > 0) range(kt - 4 + 1, kt - 4 + 2, 1);
+      if (ty > 0) {
+        const int ka = 4 * (tl.base + tile - tl.ntx);
+        range(ka + 2, ka + 3, 2);
+        if (tx > 0) range(ka - 4 + 2, ka - 4 + 2, 3);
       }
-      Chan<T, CVR>::store(dst, accum[k]);
+    } else {
+      rn[0] = uint32_t(p.Q) * uint32_t(p.P);  // every sample of the level
+    }
+    const uint32_t n01 = rn[0] + rn[1], n012 = n01 + rn[2], ncand = n012 + rn[3];
+
+    // The sample index (q * LP + s) of candidate c, or of a valid stand-in.
+    auto entry_of = [&](uint32_t c) __attribute__((always_inline)) -> uint32_t {
+      if (c >= ncand) c = 0;
+      if (ncand == 0) return uint32_t(l * p.P);
+      if (!bucketed) {
+        const uint32_t q = fdiv(c, bg.div_p), pt = c - q * uint32_t(p.P);
+        return q * uint32_t(LP) + uint32_t(l * p.P) + pt;
+      }
+      const uint32_t idx = c < rn[0] ? rs[0] + c
+                           : c < n01 ? rs[1] + (c - rn[0])
+                           : c < n012 ? rs[2] + (c - n01)
+                                      : rs[3] + (c - n012);
+      return ent[idx];
+    };
+
+    A accum[kOwnerItems][CVR];
+#pragma unroll
+    for (int k = 0; k < kOwnerItems; ++k)
+#pragma unroll
+      for (int c = 0; c < CVR; ++c) accum[k][c] = A(0);
+
+    const uint32_t nbatch = (ncand + uint32_t(nb) - 1) / uint32_t(nb);
+    const uint32_t own = uint32_t(tid < nb ? tid : 0);
+    // Pipeline registers: `f_*` data of the next batch, `e_next` the own sample
+    // index of the next batch, `e_after` that of the batch after it.
+    LocPair<TL> f_loc{}, c_loc{};
+    T f_attn{}, c_attn{};
+    uint32_t f_own = 0, c_own = 0, e_next = 0, e_after = 0;
+    PieceT f_piece[kOwnerChunks];
+    auto issue = [&](uint32_t after_batch) __attribute__((always_inline)) {
+      f_own = e_next;
+      const uint32_t q = fdiv(f_own, bg.div_lp), s = f_own - q * uint32_t(LP);
+      const int64_t unit = unit0 + int64_t(q) * p.H;
+      f_loc = *reinterpret_cast<const LocPair<TL>*>(loc_all + (unit * LP + s) * 2);
+      if constexpr (!SOFTMAX) f_attn = attn_all[unit * LP + s];
+#pragma unroll
+      for (int k = 0; k < kOwnerChunks; ++k) {
+        const uint32_t e = qnext[prow[k] < nb ? prow[k] : 0];
+        const uint32_t qr = fdiv(e, bg.div_lp);
+        f_piece[k] = *reinterpret_cast<const PieceT*>(gout + (unit0 + int64_t(qr) * p.H) * p.D + pgrp[k] * CVR);
+      }
+      e_after = entry_of(after_batch * uint32_t(nb) + own);
+    };
+    auto retire = [&]() __attribute__((always_inline)) {
+      c_loc = f_loc;
+      c_attn = f_attn;
+      c_own = f_own;
+#pragma unroll
+      for (int k = 0; k < kOwnerChunks; ++k) {
+        if (prow[k] < nb) {
+          APiece v;
+          Chan<T, CVR>::from_raw(__builtin_bit_cast(Raw_, f_piece[k]), v.v);
+          *reinterpret_cast<APiece*>(gtile + size_t(prow[k]) * rstride + size_t(pgrp[k]) * CVR * sizeof(A)) = v;
+        }
+      }
+      if (tid < nb) qnext[tid] = e_after;
+      e_next = e_after;
+    };
+    if (nbatch > 0) {
+      // Prologue: the indices of batch 0 into qnext, then batch 0's data.
+      e_next = entry_of(own);
+      if (tid < nb) qnext[tid] = e_next;
+      lds_barrier();
+      issue(1);
+      lds_barrier();
+      retire();
+    }
+    lds_barrier();
+
+    for (uint32_t bi = 0; bi < nbatch; ++bi) {
+      issue(bi + 2);  // data of batch bi + 1, index of batch bi + 2
+      const bool has = tid < nb && bi * uint32_t(nb) + uint32_t(tid) < ncand;
+      // A. Records of the own sample.
+      int rpos[4] = {0, 0, 0, 0}, rrank[4] = {0, 0, 0, 0};
+      A rw[4] = {A(0), A(0), A(0), A(0)};
+      bool rv[4] = {false, false, false, false};
+      if (has) {
+        const Geom<A> g = geometry<A>(to_acc(c_loc.x), to_acc(c_loc.y), lv, 0u, 1u);
+        A a;
+        if constexpr (SOFTMAX) {
+          const uint32_t q = fdiv(c_own, bg.div_lp), s = c_own - q * uint32_t(LP);
+          a = unit_weight<T, true>(attn_all + (unit0 + int64_t(q) * p.H) * LP, LP, int(s));
+        } else {
+          a = to_acc(c_attn);
+        }
+        const bool m[4] = {g.m00, g.m01, g.m10, g.m11};
+        const A wb[4] = {g.w00, g.w01, g.w10, g.w11};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int cx = g.ix + (c & 1), cy = g.iy + (c >> 1);
+          rv[c] = m[c] && cx >= c0 && cx < c1 && cy >= r0 && cy < r1;
+          rpos[c] = ((cy - r0) << tl.lw) + (cx - c0);
+          rw[c] = wb[c] * a;
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (rv[c]) rrank[c] = atomicAdd(&cnt[rpos[c]], 1);
+      }
+      lds_barrier();
+      // B. Run starts.
+      {
+        int tot;
+        const int v = tid < npos ? cnt[tid] : 0;
+        const int ex = block_exclusive_scan(v, wave_sums, &tot);
+        if (tid < npos) start[tid] = ex;
+        if (tid == 0) start[npos] = tot;
+      }
+      lds_barrier();
+      // C. Place.
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (rv[c]) recs[start[rpos[c]] + rrank[c]] = TileRec<A>{rw[c], uint32_t(tid)};
+      lds_barrier();
+      // D. Accumulate, four records at a time so that their LDS reads overlap.
+#pragma unroll
+      for (int k = 0; k < kOwnerItems; ++k) {
+        const int pos = ipos[k];
+        if (pos < npos) {
+          const char* gcol = gtile + size_t(igrp[k]) * CVR * sizeof(A);
+          const int e1 = start[pos + 1];
+          int r = start[pos];
+          for (; r + 4 <= e1; r += 4) {
+            TileRec<A> rec[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) rec[u] = recs[r + u];
+            APiece gv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) gv[u] = *reinterpret_cast<const APiece*>(gcol + rec[u].slot * rstride);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+              for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec[u].w, gv[u].v[c], accum[k][c]);
+          }
+          for (; r < e1; ++r) {
+            const TileRec<A> rec = recs[r];
+            const APiece gv = *reinterpret_cast<const APiece*>(gcol + rec.slot * rstride);
+#pragma unroll
+            for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec.w, gv.v[c], accum[k][c]);
+          }
+        }
+      }
+      if (tid < npos) cnt[tid] = 0;
+      lds_barrier();
+      retire();
+      lds_barrier();
+    }
+
+    // The tile's positions: the only writer of these grad_value elements.
+    const int64_t img = int64_t(b) * p.S * p.H * p.D;
+#pragma unroll
+    for (int k = 0; k < kOwnerItems; ++k) {
+      const int pos = ipos[k];
+      const int y = r0 + (pos >> tl.lw), x = c0 + (pos & ((1 << tl.lw) - 1));
+      if (pos < npos && y < r1 && x < c1) {
+        const int64_t gpos = int64_t(lv.start) + int64_t(y) * lv.w + x;
+        char* dst = p.grad_value + (img + (gpos * p.H + h) * p.D + igrp[k] * CVR) * ES;
+        if (accumulate) {
+          A old[CVR];
+          Chan<T, CVR>::load(dst, old);
+#pragma unroll
+          for (int c = 0; c < CVR; ++c) accum[k][c] += old[c];
+        }
+        Chan<T, CVR>::store(dst, accum[k]);
+      }
     }
   }
 }
@@ -1160,14 +1407,16 @@ hipError_t dispatch(int dtype, bool loc_f32, int cv, F&& f) {
   return hipErrorInvalidValue;
 }
 
-// Launch layout of the backward's three kernels.
+// Launch layout of the backward.
 struct BackwardPlan {
-  GradValuePlan gv;
-  int gv_threads;
+  BwdGeom bg;
   int cvr;
-  size_t gv_lds;
-  int64_t gv_blocks;
-  int64_t summary_entries;
+  size_t owner_lds;
+  int64_t owner_blocks;
+  bool bucket;            // try the bucket sort (the kernels re-check on the device)
+  size_t bucket_lds;
+  int64_t bucket_chunks;  // bucketing workgroups per (b, h)
+  int64_t zero_keys;      // bucket counters to clear per (b, h)
   Plan sample;
 };
 
@@ -1180,39 +1429,28 @@ size_t device_lds_limit() {
   return size_t(bytes);
 }
 
-size_t grad_value_lds(int dtype, int threads, int64_t L, int64_t D, int qb, int64_t npos) {
-  const size_t es = size_t(elem_size(dtype));
-  const size_t rec = dtype == MSDA_F64 ? sizeof(SortedRec<double>) : sizeof(SortedRec<float>);
-  const size_t waves = size_t(threads / kWave);
-  size_t at = sizeof(Level) * size_t(L);
-  at += rec * waves * kRecordsPerWave;
-  at += (es * waves * size_t(qb) * size_t(D) + 15) & ~size_t(15);
-  at += sizeof(int) * (3 * size_t(npos) + 1);
-  at += sizeof(int) * size_t(threads);
-  at += (sizeof(int) * waves + 15) & ~size_t(15);
-  at += (dtype == MSDA_F64 ? 16 : 8) * size_t(threads);  // staged location pairs (widest case)
-  at += es * size_t(threads);                            // staged weights
+size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
+  const size_t acc = dtype == MSDA_F64 ? 8 : 4;
+  const size_t rec = dtype == MSDA_F64 ? sizeof(TileRec<double>) : sizeof(TileRec<float>);
+  size_t at = (sizeof(Level) + sizeof(LevelTiles) + sizeof(int)) * size_t(L) + sizeof(int) * size_t(L + 1);
+  at = (at + 15) & ~size_t(15);
+  at += 16;
+  at += size_t(nb) * (size_t(D) * acc + 16);
+  at += rec * size_t(4 * nb);
+  at += sizeof(uint32_t) * size_t(nb);
+  at += sizeof(int) * size_t(2 * cap + 1);
+  at += sizeof(int) * size_t(kOwnerThreads / kWave);
   return at;
 }
 
 int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, int64_t L,
                        int64_t P, int loc_dtype, const void* const* vec_ptrs, int n_vec,
-                       size_t lds_limit, BackwardPlan* plan) {
+                       const void* grad_attn, size_t lds_limit, BackwardPlan* plan) {
   int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_vec, &plan->sample);
   if (rc != MSDA_OK) return rc;
-  if (P > kWave)
-    return fail(MSDA_ERR_UNSUPPORTED, "msda: the backward takes at most %d points per level", kWave);
-  int p2_log2 = 0;
-  while ((int64_t(1) << p2_log2) < P) ++p2_log2;
-  const int qb = kWave >> p2_log2;
-  const int64_t nblocks = (Q + qb - 1) / qb;
-  const int64_t entries = B * H * L * nblocks;
-  const int64_t loc_bytes = B * Q * H * L * P * 2 * elem_size(loc_dtype);
-  if (entries * int64_t(sizeof(RowRange)) > loc_bytes)
-    return fail(MSDA_ERR_UNSUPPORTED, "msda: row summaries do not fit the location gradient");
-  // Channels per register item: the widest power of two that divides D, fits a
-  // 16-byte access and keeps grad_value aligned to it.
   const int es = elem_size(dtype);
+  // Channels per register item: the widest power of two that divides D, fits a
+  // 16-byte access and keeps grad_out and grad_value aligned to it.
   int cvr = 16 / es;
   while (cvr > 1) {
     bool ok = D % cvr == 0;
@@ -1221,72 +1459,110 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
     cvr >>= 1;
   }
   const int64_t groups = D / cvr;
+  if (groups > int64_t(kOwnerThreads) * kOwnerItems)
+    return fail(MSDA_ERR_UNSUPPORTED,
+                "msda: %lld channels per head exceed the backward's %d register items per workgroup",
+                (long long)D, kOwnerThreads * kOwnerItems);
+  BwdGeom bg = {};
+  bg.groups = int(groups);
+  bg.cap = pow2_floor(std::min<int64_t>(kOwnerThreads, int64_t(kOwnerThreads) * kOwnerItems / groups));
+  bg.amin = std::min(64, bg.cap);
+  bg.nb = pow2_floor(std::min<int64_t>(kOwnerThreads, std::max<int64_t>(1, int64_t(kOwnerThreads) * kOwnerChunks / groups)));
   const size_t budget = lds_limit < 160 * 1024 ? lds_limit : 160 * 1024;
-  int threads = kGradValueMaxThreads;
-  int64_t npos = 0;
-  for (;;) {
-    npos = std::min<int64_t>({int64_t(threads), int64_t(threads) * kItemsPerThread / groups, S});
-    if (npos >= 1 && grad_value_lds(dtype, threads, L, D, qb, npos) <= budget) break;
-    if (threads == kWave)
-      return fail(MSDA_ERR_UNSUPPORTED,
-                  "msda: %lld channels per head do not fit the backward's register and LDS budget",
-                  (long long)D);
-    threads >>= 1;
-  }
-  const int64_t nchunks = (S + npos - 1) / npos;
-  const int64_t blocks = B * H * nchunks;
-  if (blocks >= 2147483647 || nblocks >= 2147483647 || entries * kWave >= (int64_t(1) << 40))
+  while (owner_lds_bytes(dtype, L, D, bg.nb, bg.cap) > budget && bg.nb > 1) bg.nb >>= 1;
+  if (owner_lds_bytes(dtype, L, D, bg.nb, bg.cap) > budget)
+    return fail(MSDA_ERR_UNSUPPORTED, "msda: %lld levels do not fit the backward's LDS budget", (long long)L);
+  // Tiles per (b, h): every level has at most 3 h w / amin + 1 of them.
+  const int64_t tiles_bound = L + 3 * ((L * S + bg.amin - 1) / bg.amin);
+  if (tiles_bound >= (int64_t(1) << 29))
+    return fail(MSDA_ERR_UNSUPPORTED, "msda: too many backward tiles for S = %lld and L = %lld",
+                (long long)S, (long long)L);
+  bg.nw = int(std::min<int64_t>(tiles_bound, 2 * ((S + bg.cap - 1) / bg.cap) + L));
+  const int64_t samples_bh = Q * L * P;
+  bg.region = samples_bh;
+  const int64_t attn_bytes = B * samples_bh * H * es;
+  const bool attn_ok = (reinterpret_cast<uintptr_t>(grad_attn) & 3) == 0;
+  bg.keys_alloc = attn_ok && samples_bh < (int64_t(1) << 32) ? attn_bytes / (4 * B * H) : 0;
+  plan->bucket = bg.keys_alloc >= 4 * L;
+  if (!plan->bucket) bg.keys_alloc = 0;
+  plan->zero_keys = std::min<int64_t>(bg.keys_alloc, 4 * tiles_bound);
+  // Bucketing kernels: LDS counters for up to keys_lds buckets (count + base).
+  const size_t bucket_head = (((sizeof(Level) + sizeof(LevelTiles)) * size_t(L) + 15) & ~size_t(15)) + 16;
+  const int64_t want_keys = std::min<int64_t>(kBucketLdsKeys, plan->zero_keys);
+  bg.keys_lds = int(std::max<int64_t>(0, std::min<int64_t>(want_keys, int64_t(budget - std::min(budget, bucket_head)) / 4)));
+  plan->bucket_lds = bucket_head + size_t(bg.keys_lds) * 4;
+  plan->bucket_chunks = (samples_bh + kBucketThreads * kBucketSamples - 1) / (kBucketThreads * kBucketSamples);
+  plan->owner_blocks = int64_t(bg.nw) * B * H;
+  plan->owner_lds = owner_lds_bytes(dtype, L, D, bg.nb, bg.cap);
+  if (plan->owner_blocks >= 2147483647 || B * H * plan->bucket_chunks >= 2147483647 ||
+      B * S >= 2147483647)
     return fail(MSDA_ERR_UNSUPPORTED, "msda: backward grid too large");
-  plan->gv = GradValuePlan{int(npos), int(nchunks), p2_log2, int(nblocks), int(groups)};
-  plan->gv_threads = threads;
+  bg.div_lp = make_fastdiv(uint32_t(L * P));
+  bg.div_p = make_fastdiv(uint32_t(P));
+  plan->bg = bg;
   plan->cvr = cvr;
-  plan->gv_lds = grad_value_lds(dtype, threads, L, D, qb, npos);
-  plan->gv_blocks = blocks;
-  plan->summary_entries = entries;
   return MSDA_OK;
 }
 
-template <typename T, typename TL, bool SOFTMAX>
-hipError_t launch_grad_value(const BackwardPlan& plan, const Problem& p, const RowRange* rows,
-                             int accumulate, hipStream_t st) {
+template <typename Kernel>
+hipError_t allow_lds(Kernel k, size_t bytes) {
+  if (bytes <= 64 * 1024) return hipSuccess;
+  return hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                             int(bytes));
+}
+
+template <typename T, typename TL, int CVR, bool SM>
+hipError_t launch_owner(const BackwardPlan& plan, const Problem& p, const int* buckets,
+                        const uint32_t* entries, int accumulate, hipStream_t st) {
+  auto k = msda_grad_value_kernel<T, TL, CVR, SM>;
+  const hipError_t e = allow_lds(k, plan.owner_lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3(unsigned(plan.owner_blocks)), dim3(kOwnerThreads), plan.owner_lds, st, p,
+                     plan.bg, buckets, entries, accumulate);
+  return hipGetLastError();
+}
+
+template <typename T, typename TL, bool SM>
+hipError_t launch_owner_cvr(const BackwardPlan& plan, const Problem& p, const int* buckets,
+                            const uint32_t* entries, int accumulate, hipStream_t st) {
   constexpr int kMaxCv = 16 / Elem<T>::size;
-  const void* fn = nullptr;
   switch (plan.cvr) {
-    case 1: fn = reinterpret_cast<const void*>(msda_grad_value_kernel<T, TL, 1, SOFTMAX>); break;
-    case 2: fn = reinterpret_cast<const void*>(msda_grad_value_kernel<T, TL, 2, SOFTMAX>); break;
+    case 1: return launch_owner<T, TL, 1, SM>(plan, p, buckets, entries, accumulate, st);
+    case 2: return launch_owner<T, TL, 2, SM>(plan, p, buckets, entries, accumulate, st);
     case 4:
-      if constexpr (kMaxCv >= 4) fn = reinterpret_cast<const void*>(msda_grad_value_kernel<T, TL, 4, SOFTMAX>);
+      if constexpr (kMaxCv >= 4) return launch_owner<T, TL, 4, SM>(plan, p, buckets, entries, accumulate, st);
       break;
     case 8:
-      if constexpr (kMaxCv >= 8) fn = reinterpret_cast<const void*>(msda_grad_value_kernel<T, TL, 8, SOFTMAX>);
+      if constexpr (kMaxCv >= 8) return launch_owner<T, TL, 8, SM>(plan, p, buckets, entries, accumulate, st);
       break;
   }
-  if (!fn) return hipErrorInvalidValue;
-  if (plan.gv_lds > 64 * 1024) {
-    const hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, int(plan.gv_lds));
-    if (e != hipSuccess) return e;
+  return hipErrorInvalidValue;
+}
+
+// The bucket sort: clear the counters, count, scan, place.
+template <typename TL>
+hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* buckets, uint32_t* entries,
+                          hipStream_t st) {
+  const int64_t clear_bytes = int64_t(p.B) * p.H * plan.zero_keys * 4;
+  {
+    const int64_t chunks = clear_bytes / 16 + 1;
+    const unsigned blocks = unsigned(std::min<int64_t>((chunks + 255) / 256, 4096));
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0, st, reinterpret_cast<char*>(buckets),
+                       clear_bytes);
   }
-  const dim3 grid(unsigned(plan.gv_blocks)), block(unsigned(plan.gv_threads));
-  switch (plan.cvr) {
-    case 1:
-      hipLaunchKernelGGL((msda_grad_value_kernel<T, TL, 1, SOFTMAX>), grid, block, plan.gv_lds, st, p,
-                         plan.gv, rows, accumulate);
-      break;
-    case 2:
-      hipLaunchKernelGGL((msda_grad_value_kernel<T, TL, 2, SOFTMAX>), grid, block, plan.gv_lds, st, p,
-                         plan.gv, rows, accumulate);
-      break;
-    case 4:
-      if constexpr (kMaxCv >= 4)
-        hipLaunchKernelGGL((msda_grad_value_kernel<T, TL, 4, SOFTMAX>), grid, block, plan.gv_lds, st, p,
-                           plan.gv, rows, accumulate);
-      break;
-    case 8:
-      if constexpr (kMaxCv >= 8)
-        hipLaunchKernelGGL((msda_grad_value_kernel<T, TL, 8, SOFTMAX>), grid, block, plan.gv_lds, st, p,
-                           plan.gv, rows, accumulate);
-      break;
-  }
+  const dim3 grid(unsigned(int64_t(p.B) * p.H * plan.bucket_chunks)), block(kBucketThreads);
+  auto count = msda_bucket_kernel<TL, false>;
+  auto place = msda_bucket_kernel<TL, true>;
+  hipError_t e = allow_lds(count, plan.bucket_lds);
+  if (e == hipSuccess) e = allow_lds(place, plan.bucket_lds);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(count, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
+                     int(plan.bucket_chunks));
+  const size_t scan_lds = p.L > kMaxOrderedLevels ? (sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) : 0;
+  hipLaunchKernelGGL(msda_bucket_scan_kernel, dim3(unsigned(p.B * p.H)), dim3(1024), scan_lds, st, p,
+                     plan.bg, buckets);
+  hipLaunchKernelGGL(place, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
+                     int(plan.bucket_chunks));
   return hipGetLastError();
 }
 
@@ -1369,14 +1645,14 @@ int msda_launch_geometry(int value_dtype, int64_t batch, int64_t spatial, int64_
   if (backward) {
     BackwardPlan bp;
     const int rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries,
-                                      levels, points, value_dtype, nullptr, 0, 160 * 1024, &bp);
+                                      levels, points, value_dtype, nullptr, 0, nullptr, 160 * 1024, &bp);
     if (rc != MSDA_OK) return rc;
     // The grad_value kernel's layout: channels per register item, positions per
-    // chunk, waves per workgroup and workgroups.
+    // tile at most, waves per workgroup and workgroups.
     if (channels_per_lane) *channels_per_lane = bp.cvr;
-    if (lanes_per_unit) *lanes_per_unit = bp.gv.npos;
-    if (waves_per_block) *waves_per_block = bp.gv_threads / kWave;
-    if (num_blocks) *num_blocks = bp.gv_blocks;
+    if (lanes_per_unit) *lanes_per_unit = bp.bg.cap;
+    if (waves_per_block) *waves_per_block = kOwnerThreads / kWave;
+    if (num_blocks) *num_blocks = bp.owner_blocks;
     return MSDA_OK;
   }
   Plan plan;
@@ -1469,12 +1745,12 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   if (!value || !spatial_shapes || !level_start_index || !sampling_locations ||
       !attention_weights || !grad_output)
     return fail(MSDA_ERR_INVALID, "msda_backward: null input tensor pointer");
-  if (reinterpret_cast<uintptr_t>(grad_sampling_locations) % alignof(RowRange) != 0)
+  if (reinterpret_cast<uintptr_t>(grad_sampling_locations) % 4 != 0)
     return fail(MSDA_ERR_INVALID, "msda_backward: grad_sampling_locations must be 4-byte aligned");
   const void* vec[] = {value, grad_output, grad_value};
   BackwardPlan plan;
   rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
-                          loc_dtype, vec, 2, device_lds_limit(), &plan);
+                          loc_dtype, vec, 3, grad_attention_weights, device_lds_limit(), &plan);
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,
@@ -1483,18 +1759,28 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   p.grad_value = static_cast<char*>(grad_value);
   p.grad_loc = static_cast<char*>(grad_sampling_locations);
   p.grad_attn = static_cast<char*>(grad_attention_weights);
-  RowRange* rows = static_cast<RowRange*>(grad_sampling_locations);
+  // Scratch of the bucket sort: counters in grad_attention_weights, sample indices in
+  // grad_sampling_locations; msda_grad_sample_kernel overwrites both last.
+  int* buckets = static_cast<int*>(grad_attention_weights);
+  uint32_t* entries = static_cast<uint32_t*>(grad_sampling_locations);
   const bool softmax = flags & MSDA_SOFTMAX;
   const hipError_t err = dispatch(
       value_dtype, loc_dtype == MSDA_F32 && value_dtype != MSDA_F32, plan.sample.cv,
       [&]<typename T, typename TL, int CV>() {
-        const unsigned summary_blocks = unsigned((plan.summary_entries * kWave + 255) / 256);
-        hipLaunchKernelGGL((msda_row_summary_kernel<T, TL>), dim3(summary_blocks), dim3(256), 0, st,
-                           p, plan.gv, rows);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        e = softmax ? launch_grad_value<T, TL, true>(plan, p, rows, int(accumulate), st)
-                    : launch_grad_value<T, TL, false>(plan, p, rows, int(accumulate), st);
+        hipError_t e = hipSuccess;
+        if (plan.bucket) {
+          e = launch_buckets<TL>(plan, p, buckets, entries, st);
+          if (e != hipSuccess) return e;
+        }
+        if (!accumulate) {
+          const int64_t n = int64_t(p.B) * p.S;
+          hipLaunchKernelGGL((msda_gap_zero_kernel<T>), dim3(unsigned((n + 255) / 256)), dim3(256),
+                             sizeof(Level) * size_t(p.L), st, p);
+          e = hipGetLastError();
+          if (e != hipSuccess) return e;
+        }
+        e = softmax ? launch_owner_cvr<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
+                    : launch_owner_cvr<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
         if (e != hipSuccess) return e;
         const dim3 grid(unsigned(plan.sample.num_blocks)), block(unsigned(kWave * plan.sample.waves));
         if (softmax)

@@ -121,8 +121,10 @@ def test_launch_geometry_rejects_what_the_kernels_do_not_cover(lib):
     rc, *_ = geometry(lib, 2, (1, 64, 1, 1030, 16, 1, 4), backward=False)
     assert rc == 2  # MSDA_ERR_UNSUPPORTED
     assert "channels" in lib.cdll.msda_last_error().decode().lower()
-    rc, *_ = geometry(lib, 0, (1, 64, 1, 32, 16, 1, 65), backward=True)  # > 64 points per level
+    rc, *_ = geometry(lib, 2, (1, 64, 1, 1030, 16, 1, 4), backward=True)
     assert rc == 2
+    rc, *_ = geometry(lib, 0, (1, 64, 1, 32, 16, 1, 65), backward=True)  # many points: supported
+    assert rc == 0
     rc, *_ = geometry(lib, 11, (1, 64, 1, 8, 16, 1, 4), backward=False)
     assert rc == 1
 
