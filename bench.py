@@ -6,10 +6,11 @@ config 4 (Mask2Former pixel-decoder encoder, large): B=4, levels 128x128, 64x64,
 linear method, synthetic seeded inputs already resident in HBM.
 
 Prints one JSON line: ``value`` is fwd+bwd milliseconds per call (lower is
-better); ``roofline`` rates the dominant kernel (the backward) by its algorithmic
-bytes over its own average duration, timed with HIP events on the stream it runs
-on; ``cpu_baseline`` times the torch restatement of the reference's eager CPU
-path on a bounded sample of the same workload, scaled to one full call.
+better); ``roofline`` rates the dominant launch, the backward C-ABI call (its
+kernels run back to back on one stream), by its algorithmic bytes over its average
+duration, timed with HIP events on that stream; ``cpu_baseline`` times the torch
+restatement of the reference's eager CPU path on a bounded sample of the same
+workload, scaled to one full call.
 
     python bench.py [--steps K] [--warmup W] [--dtype bf16|f16|f32] [--loc-dtype ...]
 """
@@ -72,9 +73,10 @@ def time_fwd_bwd(w, steps: int, warmup: int, softmax: bool):
 def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
     """Average device time of each direction alone, through the C ABI, on torch's stream.
 
-    The forward is one kernel; the backward is one kernel for the linear method
-    (the owner-computes grad_value kernel, which also writes the location and
-    weight gradients), plus the softmax-Jacobian kernel for the softmax method.
+    The forward is one kernel. The backward call launches the bucket sort of the
+    samples (clear, count, scan, place), the gap zeroing, the owner-computes
+    grad_value kernel and the location / weight gradient kernel, all on this stream;
+    the events bracket the whole call.
     """
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
 
@@ -224,7 +226,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "msda_backward_owner_kernel",
+            "kernel": "msda_backward (C-ABI call: bucket sort, gap zero, grad_value, grad_sample)",
             "achieved": round(bwd_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",

@@ -2,8 +2,9 @@
 
 A drop-in for deformops' MSDA operator on AMD Instinct MI355X (gfx950): the
 ``registry.msda`` call and the ``torch.ops.deformops.msda`` / ``msda_softmax``
-operators, backed by hand-written HIP kernels (forward, and a backward that
-accumulates ``grad_value`` with atomics in place).
+operators, backed by hand-written HIP kernels: a forward, and a backward that
+writes every element of ``grad_value`` once from fp32 registers (owner-computes,
+no atomics on the gradient and no buffer beyond the three gradients).
 """
 
 from __future__ import annotations

@@ -12,8 +12,8 @@ reference's argument lists,
 each implemented for GPU tensors by one call into libdeformops_amd.so. Unlike the
 reference's float32-accumulator configuration, the backward hands the kernel the
 16-bit tensors as they are: there is no float32 upcast, no float32 scratch
-``grad_value`` and no copy back; ``grad_value`` is accumulated in place with
-atomics in its own dtype. ``chunk_step``, ``channels_per_thread`` and
+``grad_value`` and no copy back; each element of ``grad_value`` is summed in fp32
+by its one owner and stored once. ``chunk_step``, ``channels_per_thread`` and
 ``threads_per_block`` are accepted and ignored (the kernels pick their own layout);
 ``K`` must equal the points axis of ``loc``.
 """

@@ -1,33 +1,32 @@
 // Multi-scale deformable attention (MSDA) for AMD Instinct MI355X (gfx950):
 // forward and zero-buffer backward behind the C ABI of include/deformops_amd.h.
 //
-// Work decomposition. A "unit" is one (batch, query, head): it owns the D channels
-// of one output vector and L * P samples. A unit is served by LH = 2^k lanes of a
-// wave64, each lane holding CV consecutive channels (CV * element size <= 16 bytes,
-// so one corner fetch is one global_load_dwordx4 for bf16/f16 D = 32). A wave
-// therefore serves UW = 64 / LH units; a workgroup is 1-4 waves. Workgroups are
-// renumbered so that consecutive units land on the same XCD (gfx950 deals
-// workgroups to its 8 XCDs round-robin, and each XCD has its own L2): queries that
-// are neighbours in the flattened pyramid sample neighbouring pixels, so this keeps
-// their corner gathers and grad_value atomics inside one L2.
-//
-// Each kernel runs in phases:
+// Sample-parallel kernels (the forward, and the location / weight gradients of the
+// backward). A "unit" is one (batch, query, head): it owns the D channels of one
+// output vector and L * P samples. A unit is served by LH = 2^k lanes of a wave64,
+// each lane holding CV consecutive channels (CV * element size <= 16 bytes, so one
+// corner fetch is one global_load_dwordx4 for bf16/f16 D = 32). A wave therefore
+// serves UW = 64 / LH units; a workgroup is 1-4 waves. Workgroups are renumbered so
+// that consecutive units land on the same XCD (gfx950 deals workgroups to its 8
+// XCDs round-robin, and each XCD has its own L2): queries that are neighbours in
+// the flattened pyramid sample neighbouring pixels, so their corner gathers share
+// one L2. Each such kernel runs in phases:
 //   1. Every lane of a unit takes samples s = t, t + LH, ... (t = lane in unit),
 //      reads its location and weight, and stages the sample's four corner byte
 //      offsets and four (bilinear * attention) weights in LDS. The softmax over the
 //      L * P weights of a unit is a cross-lane max / sum inside the unit's lanes.
 //   2. The unit's lanes walk all L * P samples: one broadcast LDS read of the
-//      staged sample, four vector corner loads, fp32 (fp64 for double) FMAs.
-//      The backward also forms the four per-corner dot products
-//      G_c = sum_d grad_out[d] * value_c[d], reduces them across the unit's lanes,
-//      and scatters grad_out * weight into grad_value with global atomics in the
-//      value dtype (global_atomic_pk_add_bf16 / pk_add_f16 / add_f32 / add_f64).
+//      staged sample, four vector corner loads, fp32 (fp64 for double) FMAs. The
+//      backward forms the four per-corner dot products
+//      G_c = sum_d grad_out[d] * value_c[d] instead and reduces them across the
+//      unit's lanes.
 //   3. (backward) The lane that staged sample s turns its G_c into the location
 //      and weight gradients:
 //        dL/dw   = sum_c bilinear_c * G_c
 //        dL/dx   = a * W * ((1 - dy) (G01 - G00) + dy (G11 - G10))
 //        dL/dy   = a * H * ((1 - dx) (G10 - G00) + dx (G11 - G01))
 //      and, for the softmax method, dL/dlogit_j = p_j (dL/dp_j - sum_i p_i dL/dp_i).
+// grad_value is owner-computed by tile kernels instead; see the backward section.
 //
 // Semantics follow the reference eager backend
 // (sources/deformops/backends/eager/msda_pytorch.py:23-112): pixel = loc * size -
@@ -834,10 +833,30 @@ template <> struct PieceOf<8> { using type = u32x2_v; };
 template <> struct PieceOf<16> { using type = u32x4_v; };
 template <typename T, int CVR> using Piece = typename PieceOf<Elem<T>::size * CVR>::type;
 
-// grad_out rows are staged in LDS in the accumulation type, CVR values per piece.
-template <typename A, int CVR> struct alignas(CVR * sizeof(A) < 16 ? CVR * sizeof(A) : 16) AccPiece {
-  A v[CVR];
-};
+// Exclusive prefix sum of n <= 4 * 64 counters by one wave (four per lane, DPP scan
+// of the lane totals); writes start[0..n] and clears the counters.
+__device__ inline void wave_scan_counts(int* cnt, int* start, int n) {
+  const int lane = threadIdx.x & (kWave - 1);
+  int v[4], sum = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = lane * 4 + j;
+    v[j] = i < n ? cnt[i] : 0;
+    sum += v[j];
+  }
+  const int inc = wave_inclusive_scan(sum);
+  int run = inc - sum;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = lane * 4 + j;
+    if (i < n) {
+      start[i] = run;
+      cnt[i] = 0;
+    }
+    run += v[j];
+  }
+  if (lane == kWave - 1) start[n] = inc;
+}
 
 // Owner-computes grad_value. Workgroup (slot, b, h) takes tiles slot, slot + nw, ...
 // of (b, h) in descending order of expected records per tile. For each tile, batches
@@ -845,30 +864,29 @@ template <typename A, int CVR> struct alignas(CVR * sizeof(A) < 16 ? CVR * sizeo
 //   A. thread t < nb turns candidate t into up to four corner records (position in
 //      the tile, its sample slot, attention * bilinear weight) and ranks each record
 //      within its position with an LDS integer atomic on the histogram;
-//   B. an exclusive scan of the histogram gives each position's run;
+//   B. one wave scans the histogram into each position's run (and clears it);
 //   C. records move to run start + rank;
 //   D. each thread walks the runs of the (position, channel group) items it owns
-//      and accumulates weight * grad_out, four records at a time, from grad_out
-//      rows staged in LDS (converted to the accumulation type once, when staged).
-// Software pipeline: the sample index of every candidate of the next batch sits in
-// LDS (`qnext`); at the top of a batch each thread loads its next sample's location
-// and weight and its share of the next batch's grad_out rows, and the index of its
-// sample two batches ahead; these arrive while the batch is processed and move to
-// LDS / registers after it.
+//      and accumulates weight * grad_out into fp32 registers, four records at a
+//      time, from the batch's grad_out rows staged in LDS.
+// Pipeline, three barriers per batch: after A each thread loads its sample of the
+// next batch (location, weight) and its share of the next batch's grad_out rows
+// (whose sample indices wait in LDS, `qnext`), plus its sample index two batches
+// ahead; after D it moves them to registers and to the other of two grad_out row
+// buffers. The loads are in flight during B, C and D.
 template <typename T, typename TL, int CVR, bool SOFTMAX>
 __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
     const Problem p, const BwdGeom bg, const int* __restrict__ buckets,
     const uint32_t* __restrict__ entries, const int accumulate) {
   using A = typename Elem<T>::acc;
   using PieceT = Piece<T, CVR>;
-  using Raw_ = Raw<Elem<T>::size * CVR>;
-  using APiece = AccPiece<A, CVR>;
   constexpr int ES = Elem<T>::size;
+  constexpr int PB = ES * CVR;
   extern __shared__ __align__(16) unsigned char smem[];
-  const int tid = threadIdx.x;
+  const int tid = threadIdx.x, wave = tid / kWave;
   const int G = bg.groups, nb = bg.nb, cap = bg.cap;
   const int LP = p.L * p.P;
-  const size_t rstride = size_t(p.D) * sizeof(A) + 16;  // padded: fewer bank conflicts
+  const size_t rstride = size_t(p.D) * ES + 16;  // padded rows: fewer bank conflicts
 
   // LDS layout; every offset is an integer added to smem, so accesses stay ds_*.
   size_t at = 0;
@@ -883,8 +901,9 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
   at = (at + 15) & ~size_t(15);
   int64_t* total = reinterpret_cast<int64_t*>(smem + at);
   at += 16;
-  char* gtile = reinterpret_cast<char*>(smem + at);  // nb staged grad_out rows
-  at += size_t(nb) * rstride;
+  char* gtile = reinterpret_cast<char*>(smem + at);  // two buffers of nb grad_out rows
+  const size_t gbuf = size_t(nb) * rstride;
+  at += 2 * gbuf;
   TileRec<A>* recs = reinterpret_cast<TileRec<A>*>(smem + at);
   at += sizeof(TileRec<A>) * size_t(4 * nb);
   uint32_t* qnext = reinterpret_cast<uint32_t*>(smem + at);  // next batch's sample indices
@@ -892,8 +911,6 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
   int* cnt = reinterpret_cast<int*>(smem + at);
   at += sizeof(int) * size_t(cap);
   int* start = reinterpret_cast<int*>(smem + at);  // cap + 1 entries
-  at += sizeof(int) * size_t(cap + 1);
-  int* wave_sums = reinterpret_cast<int*>(smem + at);
 
   const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
   if (ntiles <= 0) return;
@@ -1030,18 +1047,17 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
       }
       e_after = entry_of(after_batch * uint32_t(nb) + own);
     };
-    auto retire = [&]() __attribute__((always_inline)) {
+    // Move the loaded data of batch `batch` to registers and its grad_out rows to
+    // their buffer; queue the indices of the batch after it.
+    auto retire = [&](uint32_t batch) __attribute__((always_inline)) {
       c_loc = f_loc;
       c_attn = f_attn;
       c_own = f_own;
+      char* buf = gtile + (batch & 1) * gbuf;
 #pragma unroll
-      for (int k = 0; k < kOwnerChunks; ++k) {
-        if (prow[k] < nb) {
-          APiece v;
-          Chan<T, CVR>::from_raw(__builtin_bit_cast(Raw_, f_piece[k]), v.v);
-          *reinterpret_cast<APiece*>(gtile + size_t(prow[k]) * rstride + size_t(pgrp[k]) * CVR * sizeof(A)) = v;
-        }
-      }
+      for (int k = 0; k < kOwnerChunks; ++k)
+        if (prow[k] < nb)
+          *reinterpret_cast<PieceT*>(buf + size_t(prow[k]) * rstride + size_t(pgrp[k]) * PB) = f_piece[k];
       if (tid < nb) qnext[tid] = e_after;
       e_next = e_after;
     };
@@ -1052,12 +1068,11 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
       lds_barrier();
       issue(1);
       lds_barrier();
-      retire();
+      retire(0);
     }
     lds_barrier();
 
     for (uint32_t bi = 0; bi < nbatch; ++bi) {
-      issue(bi + 2);  // data of batch bi + 1, index of batch bi + 2
       const bool has = tid < nb && bi * uint32_t(nb) + uint32_t(tid) < ncand;
       // A. Records of the own sample.
       int rpos[4] = {0, 0, 0, 0}, rrank[4] = {0, 0, 0, 0};
@@ -1086,14 +1101,9 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
           if (rv[c]) rrank[c] = atomicAdd(&cnt[rpos[c]], 1);
       }
       lds_barrier();
-      // B. Run starts.
-      {
-        int tot;
-        const int v = tid < npos ? cnt[tid] : 0;
-        const int ex = block_exclusive_scan(v, wave_sums, &tot);
-        if (tid < npos) start[tid] = ex;
-        if (tid == 0) start[npos] = tot;
-      }
+      issue(bi + 2);  // data of batch bi + 1, index of batch bi + 2
+      // B. Run starts (one wave), counters cleared for the next batch.
+      if (wave == 0) wave_scan_counts(cnt, start, npos);
       lds_barrier();
       // C. Place.
 #pragma unroll
@@ -1101,38 +1111,40 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
         if (rv[c]) recs[start[rpos[c]] + rrank[c]] = TileRec<A>{rw[c], uint32_t(tid)};
       lds_barrier();
       // D. Accumulate, four records at a time so that their LDS reads overlap.
+      const char* cur = gtile + (bi & 1) * gbuf;
 #pragma unroll
       for (int k = 0; k < kOwnerItems; ++k) {
         const int pos = ipos[k];
         if (pos < npos) {
-          const char* gcol = gtile + size_t(igrp[k]) * CVR * sizeof(A);
+          const char* gcol = cur + size_t(igrp[k]) * PB;
           const int e1 = start[pos + 1];
           int r = start[pos];
           for (; r + 4 <= e1; r += 4) {
             TileRec<A> rec[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) rec[u] = recs[r + u];
-            APiece gv[4];
+            A gv[4][CVR];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) gv[u] = *reinterpret_cast<const APiece*>(gcol + rec[u].slot * rstride);
+            for (int u = 0; u < 4; ++u) Chan<T, CVR>::load(gcol + rec[u].slot * rstride, gv[u]);
 #pragma unroll
             for (int u = 0; u < 4; ++u)
 #pragma unroll
-              for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec[u].w, gv[u].v[c], accum[k][c]);
+              for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec[u].w, gv[u][c], accum[k][c]);
           }
           for (; r < e1; ++r) {
             const TileRec<A> rec = recs[r];
-            const APiece gv = *reinterpret_cast<const APiece*>(gcol + rec.slot * rstride);
+            A gv[CVR];
+            Chan<T, CVR>::load(gcol + rec.slot * rstride, gv);
 #pragma unroll
-            for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec.w, gv.v[c], accum[k][c]);
+            for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec.w, gv[c], accum[k][c]);
           }
         }
       }
-      if (tid < npos) cnt[tid] = 0;
-      lds_barrier();
-      retire();
-      lds_barrier();
+      // Batch bi + 1 into the other buffer (last read by batch bi - 1, which every
+      // wave finished before this batch's first barrier).
+      retire(bi + 1);
     }
+    lds_barrier();  // the last batch's reads are done before the next tile's prologue
 
     // The tile's positions: the only writer of these grad_value elements.
     const int64_t img = int64_t(b) * p.S * p.H * p.D;
@@ -1430,16 +1442,15 @@ size_t device_lds_limit() {
 }
 
 size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
-  const size_t acc = dtype == MSDA_F64 ? 8 : 4;
+  const size_t es = size_t(elem_size(dtype));
   const size_t rec = dtype == MSDA_F64 ? sizeof(TileRec<double>) : sizeof(TileRec<float>);
   size_t at = (sizeof(Level) + sizeof(LevelTiles) + sizeof(int)) * size_t(L) + sizeof(int) * size_t(L + 1);
   at = (at + 15) & ~size_t(15);
   at += 16;
-  at += size_t(nb) * (size_t(D) * acc + 16);
+  at += 2 * size_t(nb) * (size_t(D) * es + 16);
   at += rec * size_t(4 * nb);
   at += sizeof(uint32_t) * size_t(nb);
   at += sizeof(int) * size_t(2 * cap + 1);
-  at += sizeof(int) * size_t(kOwnerThreads / kWave);
   return at;
 }
 

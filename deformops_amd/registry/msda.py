@@ -262,7 +262,9 @@ def _msda_call(  # noqa: PLR0913
     Notes
     -----
     float32, float16, bfloat16 and float64 values run on the GPU. ``grad_value`` is
-    accumulated with atomics in the value dtype straight into the gradient tensor.
+    summed in fp32 (fp64 for float64) by the single owner of each element and
+    stored once in the value dtype; the backward uses no memory beyond the three
+    gradient tensors.
     """
     raise NotImplementedError
 

@@ -93,12 +93,18 @@ int msda_forward(const void* value, int value_dtype,
  *   grad_sampling_locations  [B, Q, H, L, P, 2]  loc_dtype
  *   grad_attention_weights   [B, Q, H, L * P]    value_dtype (w.r.t. the logits
  *                                                 under MSDA_SOFTMAX)
- * grad_value is zero-filled by this call (by a kernel, not hipMemsetAsync, so the
- * call may be captured in a HIP graph) unless flags has MSDA_ACCUMULATE_GRAD_VALUE,
- * and is then accumulated with device-scope atomics in its own dtype (packed bf16
- * / f16 atomics for 16-bit values): no scratch buffer and no float32 copy. The
- * summation order, and so the last bits of grad_value, vary between runs. The other
- * two gradients are written in full, zeros included.
+ * Every element of grad_value is written exactly once, by the one thread that
+ * owns it, from an fp32 (fp64 for MSDA_F64) register sum of all its contributions;
+ * with MSDA_ACCUMULATE_GRAD_VALUE the previous contents are added to that sum. No
+ * atomics touch grad_value, it needs no zero-fill, and there is no float32 copy.
+ * The order in which an element's contributions are summed, and so the last bits of
+ * grad_value, may vary between runs. The other two gradients are written in full,
+ * zeros included. While the call runs, grad_sampling_locations and
+ * grad_attention_weights serve as its scratch (a bucket sort of the samples by
+ * pyramid tile); they are overwritten with the gradients before it completes. So
+ * the call needs no memory beyond its outputs, and the three gradient buffers
+ * must not alias each other or the inputs. grad_sampling_locations must be 4-byte
+ * aligned.
  *
  * Replaces deformops_cuda::msda_fp32acc[_softmax]_backward
  * (sources/deformops/backends/cuda/_schema.py:24-29, include/msda_boxed.cuh:32-53,

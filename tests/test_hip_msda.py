@@ -5,7 +5,7 @@ autograd backward) on the GPU, and compares with the float64 C oracle on the sam
 (rounded) inputs, norm-wise: ``max|actual - expected| / max|expected|`` (the form
 of the reference's tests/deformops/test_msda_shared_reduction_gpu.py:75-77).
 Tolerances: float32 forward 1e-5, float32 backward 1e-4
-(atomic summation order varies), bfloat16 / float16 2e-2 of the float64 result on
+(the summation order of grad_value varies), bfloat16 / float16 2e-2 of the float64 result on
 the rounded inputs; float64 1e-10.
 """
 
@@ -348,11 +348,11 @@ def test_malformed_level_table_reads_nothing_out_of_bounds(device):
     assert rel_err(out, ref) <= 1e-5
 
 
-# Precision of the native-dtype atomics.
+# Precision of the 16-bit gradients: fp32 sums rounded once, so no drift.
 
 
 @pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
-def test_grad_value_atomics_are_unbiased(device, dtype):
+def test_grad_value_is_unbiased(device, dtype):
     """|cos(mean error, fp64 gradient)| < 0.05 over 4 runs
     (reference tests/deformops/test_msda_bias.py:23-109)."""
     levels = ((48, 48), (24, 24), (12, 12))
