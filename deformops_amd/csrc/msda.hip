@@ -113,6 +113,12 @@ template <int CV> struct Chan<float, CV> {
   static __device__ inline void load(const char* p, float (&v)[CV]) {
     from_raw(*reinterpret_cast<const R*>(p), v);
   }
+  // acc + sum_i a[i] * b[i] over the CV channels.
+  static __device__ inline float dot(const R& a, const R& b, float acc) {
+#pragma unroll
+    for (int i = 0; i < CV; ++i) acc = fma(__uint_as_float(a.w[i]), __uint_as_float(b.w[i]), acc);
+    return acc;
+  }
   static __device__ inline void store(char* p, const float (&v)[CV]) {
     R r;
 #pragma unroll
@@ -135,6 +141,14 @@ template <int CV> struct Chan<double, CV> {
   }
   static __device__ inline void load(const char* p, double (&v)[CV]) {
     from_raw(*reinterpret_cast<const R*>(p), v);
+  }
+  static __device__ inline double dot(const R& a, const R& b, double acc) {
+    double x[CV], y[CV];
+    from_raw(a, x);
+    from_raw(b, y);
+#pragma unroll
+    for (int i = 0; i < CV; ++i) acc = fma(x[i], y[i], acc);
+    return acc;
   }
   static __device__ inline void store(char* p, const double (&v)[CV]) {
     R r;
@@ -182,6 +196,25 @@ template <typename T, int CV> struct Chan16 {
   static __device__ inline void load(const char* p, float (&v)[CV]) {
     from_raw(*reinterpret_cast<const R*>(p), v);
   }
+  // acc + sum_i a[i] * b[i]: packed dot products (v_dot2c_f32_bf16 / _f16) on the
+  // raw pairs. A product of two 16-bit values is exact in fp32, so this equals
+  // widening both and accumulating with FMAs up to fp32 rounding.
+  static __device__ inline float dot(const R& a, const R& b, float acc) {
+    if constexpr (CV == 1) {
+      return fma(lo(a.h), lo(b.h), acc);
+    } else {
+#pragma unroll
+      for (int i = 0; i < CV / 2; ++i) {
+        if constexpr (kBf16)
+          acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a.w[i]),
+                                                __builtin_bit_cast(bf16x2_v, b.w[i]), acc, false);
+        else
+          acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_v, a.w[i]), __builtin_bit_cast(f16x2_v, b.w[i]),
+                                       acc, false);
+      }
+      return acc;
+    }
+  }
   static __device__ inline void store(char* p, const float (&v)[CV]) {
     R r;
     if constexpr (CV == 1) {
@@ -213,11 +246,33 @@ template <int CV> struct Chan<f16_t, CV> : Chan16<f16_t, CV> {};
 // Cross-lane reductions inside the LH lanes of one unit (LH a power of two, the
 // unit's lanes contiguous and aligned). Every lane of the wave must call them.
 
+// Units of up to four lanes (bf16 / f16 D = 32 takes four) use DPP quad
+// permutations, which stay in the VALU; wider units go through ds_bpermute.
+template <int CTRL> __device__ inline float quad_perm(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+constexpr int kQuadXor1 = 0xb1;  // quad_perm [1, 0, 3, 2]
+constexpr int kQuadXor2 = 0x4e;  // quad_perm [2, 3, 0, 1]
+
 template <typename A> __device__ inline A unit_sum(A v, int lh) {
+  if constexpr (__is_same(A, float)) {
+    if (lh <= 4) {
+      if (lh >= 2) v += quad_perm<kQuadXor1>(v);
+      if (lh >= 4) v += quad_perm<kQuadXor2>(v);
+      return v;
+    }
+  }
   for (int m = 1; m < lh; m <<= 1) v += __shfl_xor(v, m, kWave);
   return v;
 }
 template <typename A> __device__ inline A unit_max(A v, int lh) {
+  if constexpr (__is_same(A, float)) {
+    if (lh <= 4) {
+      if (lh >= 2) v = fmax(v, quad_perm<kQuadXor1>(v));
+      if (lh >= 4) v = fmax(v, quad_perm<kQuadXor2>(v));
+      return v;
+    }
+  }
   for (int m = 1; m < lh; m <<= 1) v = fmax(v, __shfl_xor(v, m, kWave));
   return v;
 }
@@ -332,6 +387,31 @@ __device__ inline Geom<A> geometry(A lx, A ly, const Level lv, uint32_t head_byt
   return g;
 }
 
+// XCD-aware renumbering: hardware workgroup i runs on XCD i % 8. Returns a logical
+// index such that each XCD runs one contiguous range of logical workgroups, so
+// workgroups that share cache lines (neighbouring queries, the heads of one query)
+// share that XCD's L2.
+__device__ inline int xcd_logical_block() {
+  const int n = int(gridDim.x), per = n / kXcds, rem = n % kXcds;
+  const int xcd = int(blockIdx.x) % kXcds, slot = int(blockIdx.x) / kXcds;
+  return xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+}
+
+// Grid of (group, head) workgroups where the heads of a group should share an L2:
+// group g runs on XCD g % 8, its H heads back to back; groups reach each XCD in
+// increasing order. The grid is padded to a multiple of 8 * H; returns false for
+// the padding.
+__device__ inline bool xcd_group_block(int H, int ngroups, int* group, int* head) {
+  const int xcd = int(blockIdx.x) % kXcds, k = int(blockIdx.x) / kXcds;
+  *head = k % H;
+  *group = (k / H) * kXcds + xcd;
+  return *group < ngroups;
+}
+
+int64_t xcd_group_grid(int64_t H, int64_t ngroups) {
+  return (ngroups + kXcds - 1) / kXcds * kXcds * H;
+}
+
 // Block-invariant facts of one lane.
 struct LaneMap {
   int lane, wave, t, uw, lh, uw_count;
@@ -349,11 +429,7 @@ __device__ inline LaneMap map_lane(const Problem& p) {
   m.uw_count = kWave >> p.lh_log2;
   m.t = m.lane & (m.lh - 1);
   m.uw = m.lane >> p.lh_log2;
-  // XCD-aware renumbering: hardware workgroup i runs on XCD i % 8; give XCD x a
-  // contiguous range of logical workgroups.
-  const int n = p.num_blocks, per = n / kXcds, rem = n % kXcds;
-  const int xcd = int(blockIdx.x) % kXcds, slot = int(blockIdx.x) / kXcds;
-  const int blk = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+  const int blk = xcd_logical_block();
   m.b = blk / p.blocks_per_batch;
   m.unit = (blk - m.b * p.blocks_per_batch) * p.units_per_block + m.wave * m.uw_count + m.uw;
   m.unit_ok = m.unit < p.Q * p.H;
@@ -692,9 +768,13 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket_kernel(const Probl
   const int64_t nkeys = 4 * ntiles;
   if (ntiles < 0 || nkeys > bg.keys_alloc) return;  // no bucketing: the owners scan
   const bool in_lds = nkeys <= bg.keys_lds;
-  const int bh = int(blockIdx.x) / chunks_per_bh;
-  const int chunk = int(blockIdx.x) - bh * chunks_per_bh;
-  const int b = bh / p.H, h = bh - b * p.H;
+  // Groups (b, chunk), the heads of a group on one XCD: they share the cache lines of
+  // their queries' locations.
+  int group, h;
+  if (!xcd_group_block(p.H, p.B * chunks_per_bh, &group, &h)) return;
+  const int chunk = group % chunks_per_bh;
+  const int b = group / chunks_per_bh;
+  const int bh = b * p.H + h;
   const int LP = p.L * p.P;
   const int64_t nsamples = int64_t(p.Q) * LP;
   int* bucket_row = buckets + int64_t(bh) * nkeys;
@@ -809,7 +889,7 @@ __global__ __launch_bounds__(256) void msda_gap_zero_kernel(const Problem p) {
 
 template <typename A> struct alignas(8) TileRec {
   A w;
-  uint32_t slot;
+  uint32_t off;  // byte offset of the record's staged grad_out row
 };
 
 // Raw (unconverted) loads for the prefetch, so that it does not wait for its data.
@@ -832,6 +912,49 @@ template <> struct PieceOf<4> { using type = uint32_t; };
 template <> struct PieceOf<8> { using type = u32x2_v; };
 template <> struct PieceOf<16> { using type = u32x4_v; };
 template <typename T, int CVR> using Piece = typename PieceOf<Elem<T>::size * CVR>::type;
+
+// How the owner kernel adds one corner record (weight w, staged grad_out piece g)
+// into its CVR accumulators: acc[c] += w * g[c].
+template <typename T, int CVR> struct OwnerAdd {
+  using A = typename Elem<T>::acc;
+  using Rec = TileRec<A>;
+  static __device__ inline Rec make(A w, uint32_t off) { return Rec{w, off}; }
+  static __device__ inline void add(A (&acc)[CVR], const Rec& r, const Piece<T, CVR>& pc) {
+    A g[CVR];
+    Chan<T, CVR>::from_raw(__builtin_bit_cast(Raw<Elem<T>::size * CVR>, pc), g);
+#pragma unroll
+    for (int c = 0; c < CVR; ++c) acc[c] = fma(r.w, g[c], acc[c]);
+  }
+};
+
+// bfloat16 pairs: v_dot2c_f32_bf16 against the packed weights (w, 0) and (0, w)
+// adds w * g for the low and the high channel of a pair in one instruction each,
+// with no widening of g. The weight is rounded to bfloat16 once per record (round
+// to nearest even, unbiased, at most 2^-9 relative); products and sums stay fp32.
+// A non-finite grad_out channel also turns its pair neighbour's sum non-finite
+// (0 * inf), where widening would keep the neighbour finite.
+template <int CVR> struct OwnerAddBf16 {
+  struct alignas(8) Rec {
+    uint32_t wb;   // the weight as bfloat16, in the low half
+    uint32_t off;  // byte offset of the record's staged grad_out row
+  };
+  static __device__ inline Rec make(float w, uint32_t off) {
+    return Rec{uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(w))), off};
+  }
+  static __device__ inline void add(float (&acc)[CVR], const Rec& r, const Piece<bf16_t, CVR>& pc) {
+    const Raw<2 * CVR> g = __builtin_bit_cast(Raw<2 * CVR>, pc);
+    const bf16x2_v lo = __builtin_bit_cast(bf16x2_v, r.wb), hi = __builtin_bit_cast(bf16x2_v, r.wb << 16);
+#pragma unroll
+    for (int i = 0; i < CVR / 2; ++i) {
+      const bf16x2_v pair = __builtin_bit_cast(bf16x2_v, g.w[i]);
+      acc[2 * i] = __builtin_amdgcn_fdot2_f32_bf16(pair, lo, acc[2 * i], false);
+      acc[2 * i + 1] = __builtin_amdgcn_fdot2_f32_bf16(pair, hi, acc[2 * i + 1], false);
+    }
+  }
+};
+template <> struct OwnerAdd<bf16_t, 2> : OwnerAddBf16<2> {};
+template <> struct OwnerAdd<bf16_t, 4> : OwnerAddBf16<4> {};
+template <> struct OwnerAdd<bf16_t, 8> : OwnerAddBf16<8> {};
 
 // Exclusive prefix sum of n <= 4 * 64 counters by one wave (four per lane, DPP scan
 // of the lane totals); writes start[0..n] and clears the counters.
@@ -886,7 +1009,7 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
   const int tid = threadIdx.x, wave = tid / kWave;
   const int G = bg.groups, nb = bg.nb, cap = bg.cap;
   const int LP = p.L * p.P;
-  const size_t rstride = size_t(p.D) * ES + 16;  // padded rows: fewer bank conflicts
+  const uint32_t rstride = uint32_t(p.D) * ES + 16;  // padded rows: fewer bank conflicts
 
   // LDS layout; every offset is an integer added to smem, so accesses stay ds_*.
   size_t at = 0;
@@ -902,10 +1025,12 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
   int64_t* total = reinterpret_cast<int64_t*>(smem + at);
   at += 16;
   char* gtile = reinterpret_cast<char*>(smem + at);  // two buffers of nb grad_out rows
-  const size_t gbuf = size_t(nb) * rstride;
+  const uint32_t gbuf = uint32_t(nb) * rstride;
   at += 2 * gbuf;
-  TileRec<A>* recs = reinterpret_cast<TileRec<A>*>(smem + at);
-  at += sizeof(TileRec<A>) * size_t(4 * nb);
+  using Add = OwnerAdd<T, CVR>;
+  using Rec = typename Add::Rec;
+  Rec* recs = reinterpret_cast<Rec*>(smem + at);
+  at += sizeof(Rec) * size_t(4 * nb);
   uint32_t* qnext = reinterpret_cast<uint32_t*>(smem + at);  // next batch's sample indices
   at += sizeof(uint32_t) * size_t(nb);
   int* cnt = reinterpret_cast<int*>(smem + at);
@@ -943,10 +1068,14 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
   }
   __syncthreads();
 
-  const int nbh = p.B * p.H;
-  const int slot0 = int(blockIdx.x) / nbh;
-  const int bh = int(blockIdx.x) - slot0 * nbh;
-  const int b = bh / p.H, h = bh - b * p.H;
+  // Groups (slot, b) in slot order, the heads of a group on one XCD: they run side by
+  // side and share the cache lines of their queries' locations, weights and
+  // grad_out rows. Groups are dealt round-robin to the XCDs, heaviest tiles first.
+  int group, h;
+  if (!xcd_group_block(p.H, bg.nw * p.B, &group, &h)) return;
+  const int slot0 = group / p.B;
+  const int b = group - slot0 * p.B;
+  const int bh = b * p.H + h;
   const T* gout = reinterpret_cast<const T*>(p.grad_out);
   const T* attn_all = reinterpret_cast<const T*>(p.attn);
   const TL* loc_all = reinterpret_cast<const TL*>(p.loc);
@@ -957,11 +1086,13 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
   // Fixed per thread: the rows and channel groups of its staging pieces, and the
   // (position, channel group) items it owns.
   int prow[kOwnerChunks], pgrp[kOwnerChunks], ipos[kOwnerItems], igrp[kOwnerItems];
+  uint32_t poff[kOwnerChunks];  // LDS byte offset of each staging piece in a row buffer
 #pragma unroll
   for (int k = 0; k < kOwnerChunks; ++k) {
     const int u = tid + k * kOwnerThreads;
     prow[k] = u / G;
     pgrp[k] = u - prow[k] * G;
+    poff[k] = uint32_t(prow[k]) * rstride + uint32_t(pgrp[k] * PB);
   }
 #pragma unroll
   for (int k = 0; k < kOwnerItems; ++k) {
@@ -1057,7 +1188,7 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
 #pragma unroll
       for (int k = 0; k < kOwnerChunks; ++k)
         if (prow[k] < nb)
-          *reinterpret_cast<PieceT*>(buf + size_t(prow[k]) * rstride + size_t(pgrp[k]) * PB) = f_piece[k];
+          *reinterpret_cast<PieceT*>(buf + poff[k]) = f_piece[k];
       if (tid < nb) qnext[tid] = e_after;
       e_next = e_after;
     };
@@ -1108,7 +1239,7 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
       // C. Place.
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        if (rv[c]) recs[start[rpos[c]] + rrank[c]] = TileRec<A>{rw[c], uint32_t(tid)};
+        if (rv[c]) recs[start[rpos[c]] + rrank[c]] = Add::make(rw[c], uint32_t(tid) * uint32_t(rstride));
       lds_barrier();
       // D. Accumulate, four records at a time so that their LDS reads overlap.
       const char* cur = gtile + (bi & 1) * gbuf;
@@ -1116,27 +1247,22 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
       for (int k = 0; k < kOwnerItems; ++k) {
         const int pos = ipos[k];
         if (pos < npos) {
-          const char* gcol = cur + size_t(igrp[k]) * PB;
+          const char* gcol = cur + igrp[k] * PB;
           const int e1 = start[pos + 1];
           int r = start[pos];
           for (; r + 4 <= e1; r += 4) {
-            TileRec<A> rec[4];
+            Rec rec[4];
+            PieceT pc[4];
 #pragma unroll
             for (int u = 0; u < 4; ++u) rec[u] = recs[r + u];
-            A gv[4][CVR];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) Chan<T, CVR>::load(gcol + rec[u].slot * rstride, gv[u]);
+            for (int u = 0; u < 4; ++u) pc[u] = *reinterpret_cast<const PieceT*>(gcol + rec[u].off);
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-              for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec[u].w, gv[u][c], accum[k][c]);
+            for (int u = 0; u < 4; ++u) Add::add(accum[k], rec[u], pc[u]);
           }
           for (; r < e1; ++r) {
-            const TileRec<A> rec = recs[r];
-            A gv[CVR];
-            Chan<T, CVR>::load(gcol + rec.slot * rstride, gv);
-#pragma unroll
-            for (int c = 0; c < CVR; ++c) accum[k][c] = fma(rec.w, gv[c], accum[k][c]);
+            const Rec rec = recs[r];
+            Add::add(accum[k], rec, *reinterpret_cast<const PieceT*>(gcol + rec.off));
           }
         }
       }
@@ -1187,28 +1313,22 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
 
   // Gather the corners and form G_c; the lane that staged sample s keeps its G_c
   // in the sample's slot.
+  using R = typename Chan<T, CV>::R;
   const bool lane_ok = m.unit_ok && m.t * CV < p.D;
   const char* img = p.value + int64_t(m.b) * p.S * p.H * p.D * ES;
   const uint32_t lane_bytes = uint32_t(m.t * CV * ES);
-  A g[CV];
-  if (lane_ok) {
-    Chan<T, CV>::load(p.grad_out + (m.gunit * p.D + m.t * CV) * ES, g);
-  } else {
-#pragma unroll
-    for (int i = 0; i < CV; ++i) g[i] = A(0);
-  }
+  R g{};
+  if (lane_ok) g = *reinterpret_cast<const R*>(p.grad_out + (m.gunit * p.D + m.t * CV) * ES);
   for (int s = 0; s < LP; ++s) {
     Staged<A>* slot = wst + s * m.uw_count + m.uw;
     const Staged<A> st = *slot;
     A G[4] = {A(0), A(0), A(0), A(0)};
     if (lane_ok) {
-      A v[4][CV];
+      R v[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) Chan<T, CV>::load(img + (st.off[c] + lane_bytes), v[c]);
+      for (int c = 0; c < 4; ++c) v[c] = *reinterpret_cast<const R*>(img + (st.off[c] + lane_bytes));
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int i = 0; i < CV; ++i) G[c] = fma(g[i], v[c][i], G[c]);
+      for (int c = 0; c < 4; ++c) G[c] = Chan<T, CV>::dot(g, v[c], G[c]);
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) G[c] = unit_sum(G[c], m.lh);
@@ -1443,7 +1563,7 @@ size_t device_lds_limit() {
 
 size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
   const size_t es = size_t(elem_size(dtype));
-  const size_t rec = dtype == MSDA_F64 ? sizeof(TileRec<double>) : sizeof(TileRec<float>);
+  const size_t rec = dtype == MSDA_F64 ? sizeof(TileRec<double>) : 8;
   size_t at = (sizeof(Level) + sizeof(LevelTiles) + sizeof(int)) * size_t(L) + sizeof(int) * size_t(L + 1);
   at = (at + 15) & ~size_t(15);
   at += 16;
@@ -1503,7 +1623,7 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   bg.keys_lds = int(std::max<int64_t>(0, std::min<int64_t>(want_keys, int64_t(budget - std::min(budget, bucket_head)) / 4)));
   plan->bucket_lds = bucket_head + size_t(bg.keys_lds) * 4;
   plan->bucket_chunks = (samples_bh + kBucketThreads * kBucketSamples - 1) / (kBucketThreads * kBucketSamples);
-  plan->owner_blocks = int64_t(bg.nw) * B * H;
+  plan->owner_blocks = xcd_group_grid(H, int64_t(bg.nw) * B);
   plan->owner_lds = owner_lds_bytes(dtype, L, D, bg.nb, bg.cap);
   if (plan->owner_blocks >= 2147483647 || B * H * plan->bucket_chunks >= 2147483647 ||
       B * S >= 2147483647)
@@ -1561,7 +1681,7 @@ hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* bucke
     hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0, st, reinterpret_cast<char*>(buckets),
                        clear_bytes);
   }
-  const dim3 grid(unsigned(int64_t(p.B) * p.H * plan.bucket_chunks)), block(kBucketThreads);
+  const dim3 grid(unsigned(xcd_group_grid(p.H, int64_t(p.B) * plan.bucket_chunks))), block(kBucketThreads);
   auto count = msda_bucket_kernel<TL, false>;
   auto place = msda_bucket_kernel<TL, true>;
   hipError_t e = allow_lds(count, plan.bucket_lds);
