@@ -166,6 +166,11 @@ def main() -> int:
     parser.add_argument("--loc-dtype", choices=sorted(DTYPES), default=None)
     parser.add_argument("--method", choices=["linear", "softmax"], default="linear")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument(
+        "--copy-calibration", type=int, default=0, metavar="MIB",
+        help="first run three plain device copies of MIB MiB, the known-size reference that "
+             "scales rocprofv3's FETCH_SIZE / WRITE_SIZE counters",
+    )
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -185,6 +190,14 @@ def main() -> int:
     softmax = args.method == "softmax"
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
+    if args.copy_calibration > 0:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.randn(n, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads and writes MIB MiB
+        torch.cuda.synchronize()
+        del src, dst
     w = make_workload(4).to(device, dtype, loc_dtype)
     B, S, H, D, Q, L, P = w.sizes
     es = torch.empty((), dtype=dtype).element_size()

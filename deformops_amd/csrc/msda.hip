@@ -39,6 +39,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <stdlib.h>
+#include <type_traits>
 #include <math.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -614,6 +616,7 @@ struct BwdGeom {
   int64_t region;   // entries per (b, h): Q * L * P
   FastDiv div_lp;   // by L * P
   FastDiv div_p;    // by P
+  int sub_log2;     // > 0: every tile is 2^sub_log2 square (the matrix-core grad_value)
 };
 
 struct LevelTiles {
@@ -645,7 +648,11 @@ __device__ inline int64_t plan_tiles(const Problem& p, const BwdGeom& bg, const 
   for (int l = 0; l < p.L; ++l) {
     const Level lv = levels[l];
     LevelTiles t{0, 0, 0, 0, int(total)};
-    if (lv.ok) {
+    if (lv.ok && bg.sub_log2 > 0) {
+      t.lw = t.lh = bg.sub_log2;
+      t.ntx = (lv.w + (1 << t.lw) - 1) >> t.lw;
+      t.nty = (lv.h + (1 << t.lh) - 1) >> t.lh;
+    } else if (lv.ok) {
       const int64_t hw = int64_t(lv.h) * lv.w;
       const int64_t want = records > 0 ? int64_t(kTargetRecords) * hw / records : bg.cap;
       const int a = pow2_floor(std::min<int64_t>(std::max<int64_t>(want, bg.amin), bg.cap));
@@ -866,6 +873,26 @@ __global__ __launch_bounds__(1024) void msda_bucket_scan_kernel(const Problem p,
   }
 }
 
+// Clears the bucket counters: 4 * tiles ints per (b, h), with the tiles as the device
+// plans them (the host knows only a bound).
+__global__ __launch_bounds__(256) void msda_bucket_clear_kernel(const Problem p, const BwdGeom bg,
+                                                                int* __restrict__ buckets) {
+  __shared__ Level levels_s[kMaxOrderedLevels];
+  __shared__ LevelTiles lt_s[kMaxOrderedLevels];
+  __shared__ int64_t total_s[2];
+  extern __shared__ __align__(16) unsigned char smem[];
+  Level* levels = p.L <= kMaxOrderedLevels ? levels_s : reinterpret_cast<Level*>(smem);
+  LevelTiles* lt = p.L <= kMaxOrderedLevels ? lt_s
+                                             : reinterpret_cast<LevelTiles*>(smem + sizeof(Level) * size_t(p.L));
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total_s);
+  const int64_t nkeys = 4 * ntiles;
+  if (ntiles < 0 || nkeys > bg.keys_alloc) return;
+  // The matrix-core grad_value keeps kXcds work-queue counters right after the rows.
+  const int64_t n = int64_t(p.B) * p.H * nkeys + (bg.sub_log2 > 0 ? kXcds : 0);
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) buckets[i] = 0;
+}
+
 // Zeroes grad_value[b, pos, :, :] at every position no valid level covers; the tile
 // owners write all the others.
 template <typename T>
@@ -981,6 +1008,34 @@ __device__ inline void wave_scan_counts(int* cnt, int* start, int n) {
   if (lane == kWave - 1) start[n] = inc;
 }
 
+// Orders the levels by expected records per tile (tile area / level area), heaviest
+// first, so that the longest tiles start first, and numbers the tiles in that order:
+// the tiles of order[i] have ranks rank_base[i] .. rank_base[i + 1] - 1. One thread.
+__device__ inline void order_levels(const Problem& p, const Level* levels, const LevelTiles* lt,
+                                    int* order, int* rank_base) {
+  for (int i = 0; i < p.L; ++i) order[i] = i;
+  if (p.L <= kMaxOrderedLevels) {
+    for (int i = 0; i < p.L; ++i) {
+      int best = i;
+      for (int k = i + 1; k < p.L; ++k) {
+        const int a = order[k], c = order[best];
+        const int64_t ha = int64_t(levels[a].h) * levels[a].w, hc = int64_t(levels[c].h) * levels[c].w;
+        const int64_t ta = int64_t(1) << (lt[a].lh + lt[a].lw), tc = int64_t(1) << (lt[c].lh + lt[c].lw);
+        if (ta * hc > tc * ha) best = k;
+      }
+      const int tmp = order[i];
+      order[i] = order[best];
+      order[best] = tmp;
+    }
+  }
+  int acc_tiles = 0;
+  for (int i = 0; i < p.L; ++i) {
+    rank_base[i] = acc_tiles;
+    acc_tiles += lt[order[i]].ntx * lt[order[i]].nty;
+  }
+  rank_base[p.L] = acc_tiles;
+}
+
 // Owner-computes grad_value. Workgroup (slot, b, h) takes tiles slot, slot + nw, ...
 // of (b, h) in descending order of expected records per tile. For each tile, batches
 // of nb candidate samples:
@@ -1041,29 +1096,7 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
   if (ntiles <= 0) return;
   const bool bucketed = 4 * ntiles <= bg.keys_alloc;
   if (tid == 0) {
-    // Order the levels by expected records per tile (tile area / level area),
-    // heaviest first, so the longest workgroups start first.
-    for (int i = 0; i < p.L; ++i) order[i] = i;
-    if (p.L <= kMaxOrderedLevels) {
-      for (int i = 0; i < p.L; ++i) {
-        int best = i;
-        for (int k = i + 1; k < p.L; ++k) {
-          const int a = order[k], c = order[best];
-          const int64_t ha = int64_t(levels[a].h) * levels[a].w, hc = int64_t(levels[c].h) * levels[c].w;
-          const int64_t ta = int64_t(1) << (lt[a].lh + lt[a].lw), tc = int64_t(1) << (lt[c].lh + lt[c].lw);
-          if (ta * hc > tc * ha) best = k;
-        }
-        const int tmp = order[i];
-        order[i] = order[best];
-        order[best] = tmp;
-      }
-    }
-    int acc_tiles = 0;
-    for (int i = 0; i < p.L; ++i) {
-      rank_base[i] = acc_tiles;
-      acc_tiles += lt[order[i]].ntx * lt[order[i]].nty;
-    }
-    rank_base[p.L] = acc_tiles;
+    order_levels(p, levels, lt, order, rank_base);
     for (int i = 0; i < cap; ++i) cnt[i] = 0;
   }
   __syncthreads();
@@ -1290,6 +1323,535 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
         Chan<T, CVR>::store(dst, accum[k]);
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// grad_value on the matrix cores: 16-bit value dtypes, D = 16, 32, 48 or 64.
+//
+// Tiles are 8 x 8 positions (sub_log2 = 3), bucketed as above, each made of four
+// 4 x 4 sub-tiles. One workgroup owns one tile of one (b, h) at a time; its four
+// waves take the tile's K-blocks of 32 candidate samples round-robin and keep
+// partial sums of all four sub-tiles (16 positions x D channels each) in the fp32
+// accumulators of v_mfma_f32_16x16x32_{bf16,f16}:
+//   C_st[m, n] += sum_k W_st[m, k] * G[k, n]
+// where G[k, :] is candidate k's grad_out row and W_st[m, k] the attention *
+// bilinear weight of its corner at position m of sub-tile st (zero where it has
+// none, so a sample adds exactly its corners in the tile). Per K-block a wave
+// stages the 32 grad_out rows in its own LDS (row-major, 2 D bytes per row),
+// scatters the candidates' corner weights into four zeroed 16 x 32 weight tiles,
+// and reads the operands back: A (weights) with ds_read_b128, B (grad_out,
+// K-major) with two ds_read_b64_tr_b16 per 16 channels. Two lanes serve one
+// candidate, each one row of its 2 x 2 footprint. The weight enters the MFMA
+// rounded to 16 bits (nearest even); products and sums are fp32. Waves do not wait
+// for each other inside a tile; the loads of the next K-block (and the entries of
+// the one after) are in flight while a K-block computes. At the end of the tile the
+// four partial sums meet in LDS and wave w writes sub-tile w.
+//
+// Operand layouts of v_mfma_f32_16x16x32 (wave64; lane l, g = l / 16, i = l % 16):
+//   A: halves A[i][8 g .. 8 g + 7];  B: halves B[8 g .. 8 g + 7][i];
+//   C: floats C[4 g .. 4 g + 3][i].
+// ds_read_b64_tr_b16: inside each group of 16 lanes, lane i receives element i % 4
+// of the 8-byte rows addressed by lanes i / 4 + 4 j, j = 0..3. Lane s addresses row
+// 8 g + 4 t + s / 4 at channel 16 nb + 4 (s % 4), so lane i receives
+// G[8 g + 4 t + j][16 nb + i]: half t of its B operand for channels 16 nb .. + 15.
+//
+// A non-finite grad_out channel reaches every position of the tiles its sample is a
+// candidate of (0 * inf), not only the sample's corners.
+
+typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
+typedef float f32x4_v __attribute__((ext_vector_type(4)));
+typedef short i16x4_v __attribute__((ext_vector_type(4)));
+
+constexpr int kMfmaWaves = 4;     // waves per workgroup, splitting a tile's K-blocks
+constexpr int kMfmaSubLog2 = 3;   // 8 x 8 position tiles of four 4 x 4 sub-tiles
+constexpr int kMfmaK = 32;        // candidates per K-block: the MFMA's K
+constexpr int kMfmaMaxNb = 4;     // 16-channel column blocks: D <= 64
+constexpr int kMfmaWBytes = 16 * kMfmaK * 2;  // one 16 x 32 weight tile
+
+template <typename T> struct MfmaOp;
+template <> struct MfmaOp<bf16_t> {
+  using V = bf16x8_v;
+  static __device__ inline f32x4_v mma(V a, V b, f32x4_v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ inline uint16_t round(float w) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(w)); }
+};
+template <> struct MfmaOp<f16_t> {
+  using V = f16x8_v;
+  static __device__ inline f32x4_v mma(V a, V b, f32x4_v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ inline uint16_t round(float w) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(w)); }
+};
+
+// Keeps the compiler from moving this wave's LDS accesses across it. The LDS
+// executes one wave's instructions in order, so lanes of a wave then see each
+// other's earlier writes without a barrier.
+__device__ inline void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
+
+__device__ inline i16x4_v lds_read_tr16(const unsigned char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      reinterpret_cast<__attribute__((address_space(3))) i16x4_v*>(reinterpret_cast<uintptr_t>(p)));
+}
+
+// Per-wave LDS of the matrix-core kernel: the staged rows and the four weight
+// tiles during a tile, the wave's partial sums at its end.
+size_t mfma_wave_bytes(int64_t D) {
+  const size_t work = size_t(kMfmaK) * size_t(2 * D) + 4 * size_t(kMfmaWBytes);
+  const size_t partial = 4 * size_t(D / 16) * kWave * 16;
+  return std::max(work, partial);
+}
+
+size_t mfma_head_bytes(int64_t L) {
+  size_t at = (sizeof(Level) + sizeof(LevelTiles) + sizeof(int)) * size_t(L) + sizeof(int) * size_t(L + 1);
+  at = (at + 15) & ~size_t(15);
+  return at + 16;
+}
+
+size_t mfma_lds_bytes(int64_t L, int64_t D) { return mfma_head_bytes(L) + kMfmaWaves * mfma_wave_bytes(D); }
+
+// The candidates of one tile: ranges of the entry list (the tile's own
+// sub-buckets, then its neighbours' straddlers); candidate c sits at entry
+// c + off_k of the range k it falls in. `stand_in` is a valid sample index for
+// candidates past the end.
+struct CandRanges {
+  uint32_t n0, n01, n012, ncand;
+  uint32_t off0, off1, off2, off3;
+  uint32_t stand_in;
+};
+
+__device__ inline CandRanges tile_candidates(const int* __restrict__ brow, const LevelTiles& tl, int tile,
+                                             int tx, int ty, uint32_t stand_in) {
+  uint32_t rs[4] = {0u, 0u, 0u, 0u}, rn[4] = {0u, 0u, 0u, 0u};
+  const int kt = 4 * (tl.base + tile);
+  const uint32_t s0 = kt > 0 ? uint32_t(brow[kt - 1]) : 0u;
+  rs[0] = s0;
+  rn[0] = uint32_t(brow[kt + 3]) - s0;
+  if (tx > 0) {  // left neighbour, sub-buckets 1-2
+    rs[1] = uint32_t(brow[kt - 4]);
+    rn[1] = uint32_t(brow[kt - 2]) - rs[1];
+  }
+  if (ty > 0) {
+    const int ka = 4 * (tl.base + tile - tl.ntx);
+    rs[2] = uint32_t(brow[ka + 1]);  // tile above, sub-buckets 2-3
+    rn[2] = uint32_t(brow[ka + 3]) - rs[2];
+    if (tx > 0) {  // above-left, sub-bucket 2
+      rs[3] = uint32_t(brow[ka - 4 + 1]);
+      rn[3] = uint32_t(brow[ka - 4 + 2]) - rs[3];
+    }
+  }
+  CandRanges r;
+  r.n0 = rn[0];
+  r.n01 = rn[0] + rn[1];
+  r.n012 = r.n01 + rn[2];
+  r.ncand = r.n012 + rn[3];
+  r.off0 = rs[0];
+  r.off1 = rs[1] - r.n0;
+  r.off2 = rs[2] - r.n01;
+  r.off3 = rs[3] - r.n012;
+  r.stand_in = stand_in;
+  return r;
+}
+
+// The sample index of candidate c (candidate 0 past the end); needs ncand > 0.
+__device__ inline uint32_t cand_entry(const uint32_t* __restrict__ ent, const CandRanges r, uint32_t c) {
+  c = c < r.ncand ? c : 0u;
+  uint32_t off = r.off3;
+  off = c < r.n012 ? r.off2 : off;
+  off = c < r.n01 ? r.off1 : off;
+  off = c < r.n0 ? r.off0 : off;
+  return ent[c + off];
+}
+
+// One K-block's loads for one lane: its candidate's location and weight, and its
+// share of the block's grad_out rows (flat 16-byte piece lane + 64 j of 32 rows).
+template <typename T, typename TL, int NB> struct MfmaBlock {
+  LocPair<TL> loc;
+  T attn;
+  u32x4_v piece[NB];
+};
+
+// Per-tile constants of the matrix-core kernel (all wave-uniform).
+struct MfmaTile {
+  const char* loc;   // locations of (b, q = 0, h)
+  const char* attn;  // weights of (b, q = 0, h)
+  const char* gout;  // grad_out row of (b, q = 0, h)
+  uint32_t loc_q, attn_q, gout_q;  // bytes per query step
+  int r0, c0, r1, c1;              // tile rows [r0, r1), columns [c0, c1)
+  uint32_t ncand;
+  FastDiv div_lp;
+  int LP;
+};
+
+template <typename T, typename TL, int NB, bool SOFTMAX>
+__device__ inline void mfma_load(const MfmaTile& t, uint32_t e, int lane, MfmaBlock<T, TL, NB>& d) {
+  constexpr int kPieces = NB * 2;  // 16-byte pieces per grad_out row (2 * 16 NB bytes)
+  const uint32_t q = fdiv(e, t.div_lp), s = e - q * uint32_t(t.LP);
+  d.loc = *reinterpret_cast<const LocPair<TL>*>(t.loc + (q * t.loc_q + s * uint32_t(2 * sizeof(TL))));
+  if constexpr (!SOFTMAX) d.attn = *reinterpret_cast<const T*>(t.attn + (q * t.attn_q + s * 2u));
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int f = lane + kWave * j, row = f / kPieces, pc = f - row * kPieces;
+    const uint32_t qr = uint32_t(__shfl(int(q), row));
+    d.piece[j] = *reinterpret_cast<const u32x4_v*>(t.gout + (qr * t.gout_q + uint32_t(pc * 16)));
+  }
+}
+
+// One K-block of one wave: stage, scatter the weights, four sub-tiles of MFMAs.
+template <typename T, typename TL, int NB, bool SOFTMAX>
+__device__ inline void mfma_kblock(const MfmaTile& t, const Level& lv, uint32_t kb, uint32_t e,
+                                   const MfmaBlock<T, TL, NB>& d, int lane, unsigned char* gst,
+                                   unsigned char* wt, f32x4_v (&acc)[4][NB]) {
+  using Op = MfmaOp<T>;
+  using V = typename Op::V;
+  constexpr int kRowBytes = 32 * NB;
+  constexpr int kPieces = NB * 2;
+  const int kc = lane & (kMfmaK - 1), half = lane >> 5;
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const uint32_t c = kb * kMfmaK + uint32_t(kc);
+  // This lane's two corners: row `half` of the sample's 2 x 2 footprint, as LDS byte
+  // offsets of their weights (-1: not in the tile).
+  int o0 = -1, o1 = -1;
+  float w0 = 0.f, w1 = 0.f;
+  if (c < t.ncand) {
+    const Geom<float> g = geometry<float>(to_acc(d.loc.x), to_acc(d.loc.y), lv, 0u, 1u);
+    float a;
+    if constexpr (SOFTMAX) {
+      const uint32_t q = fdiv(e, t.div_lp), s = e - q * uint32_t(t.LP);
+      a = unit_weight<T, true>(reinterpret_cast<const T*>(t.attn + q * t.attn_q), t.LP, int(s));
+    } else {
+      a = to_acc(d.attn);
+    }
+    const int y = g.iy + half - t.r0;
+    const bool row_in = y >= 0 && g.iy + half < t.r1;
+    const bool ma = half ? g.m10 : g.m00, mb = half ? g.m11 : g.m01;
+    const float wa = half ? g.w10 : g.w00, wb = half ? g.w11 : g.w01;
+    const int x0 = g.ix - t.c0;
+    // Position (y, x) of the tile: sub-tile (y / 4) * 2 + x / 4, row (y % 4) * 4 + x % 4.
+    const int ybase = (y >> 2) * 2 * kMfmaWBytes + (y & 3) * 4 * (2 * kMfmaK) + kc * 2;
+    if (row_in && ma && x0 >= 0 && g.ix < t.c1) {
+      o0 = ybase + (x0 >> 2) * kMfmaWBytes + (x0 & 3) * (2 * kMfmaK);
+      w0 = wa * a;
+    }
+    const int x1 = x0 + 1;
+    if (row_in && mb && x1 >= 0 && g.ix + 1 < t.c1) {
+      o1 = ybase + (x1 >> 2) * kMfmaWBytes + (x1 & 3) * (2 * kMfmaK);
+      w1 = wb * a;
+    }
+  }
+  wave_lds_order();  // after the previous K-block's operand reads
+  const u32x4_v zero = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int st = 0; st < 4; ++st) *reinterpret_cast<u32x4_v*>(wt + st * kMfmaWBytes + lane * 16) = zero;
+#pragma unroll
+  for (int j = 0; j < NB; ++j) {
+    const int f = lane + kWave * j, row = f / kPieces;
+    const bool ok = kb * kMfmaK + uint32_t(row) < t.ncand;  // past the end: zero rows
+    *reinterpret_cast<u32x4_v*>(gst + f * 16) = ok ? d.piece[j] : zero;
+  }
+  wave_lds_order();
+  if (o0 >= 0) *reinterpret_cast<uint16_t*>(wt + o0) = Op::round(w0);
+  if (o1 >= 0) *reinterpret_cast<uint16_t*>(wt + o1) = Op::round(w1);
+  wave_lds_order();
+  V bv[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const unsigned char* src = gst + (8 * g16 + i16 / 4) * kRowBytes + (16 * nb + 4 * (i16 & 3)) * 2;
+    const i16x4_v t0 = lds_read_tr16(src);
+    const i16x4_v t1 = lds_read_tr16(src + 4 * kRowBytes);
+    bv[nb] = __builtin_bit_cast(V, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+  const int aoff = i16 * (2 * kMfmaK) + g16 * 16;
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+    const V av = __builtin_bit_cast(V, *reinterpret_cast<const u32x4_v*>(wt + st * kMfmaWBytes + aoff));
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[st][nb] = Op::mma(av, bv[nb], acc[st][nb]);
+  }
+}
+
+constexpr int kMfmaMaxRegions = 16;  // regions per axis at most
+constexpr int kMfmaTable = 1024;      // entries of a queue's prefix table at most
+
+// The first tile column (or row) of region r of n regions across a level `extent`
+// positions wide with `ntiles` tiles: tile t, centred at position S t + S / 2 (S =
+// the tile side), lies in region floor((S t + S / 2) n / extent).
+__device__ inline int region_first_tile(int r, int n, int extent, int ntiles) {
+  if (r >= n) return ntiles;
+  constexpr int S = 1 << kMfmaSubLog2;
+  const int64_t num = int64_t(r) * extent - int64_t(S / 2) * n;
+  if (num <= 0) return 0;
+  const int64_t den = int64_t(S) * n;
+  return int(std::min<int64_t>(ntiles, (num + den - 1) / den));
+}
+
+// Work distribution: a persistent grid with one work queue per XCD (a counter in
+// the scratch after the bucket counters; workgroup w serves queue w % 8, the XCD the
+// dispatcher deals it to). The image is cut into RX x RY regions in normalized
+// coordinates, and a tile of any level belongs to the region of its centre: the
+// tiles of one region at all levels gather nearly the same queries, because a
+// query samples every level at the same normalized place. Queue x holds the x-th
+// eighth of the (b, region) pairs; per pair the tasks (tile, h) run level by level,
+// heaviest tiles first, heads fastest. So an XCD's workgroups share one compact
+// neighbourhood of queries in their L2 at a time, and a workgroup that finishes
+// early takes the next task of its queue. A small LDS table of prefix counts per
+// (pair, level) maps a queue position to its task. When the table would not fit,
+// queue x holds the x-th eighth of each level's tasks (b, tile, h) in raster order.
+template <typename T, typename TL, int NB, bool SOFTMAX>
+__global__ __launch_bounds__(kWave * kMfmaWaves, NB <= 2 ? 4 : 2) void msda_grad_value_mfma_kernel(
+    const Problem p, const BwdGeom bg, int* __restrict__ buckets,
+    const uint32_t* __restrict__ entries, const int accumulate) {
+  constexpr int D = 16 * NB;
+  constexpr int ES = 2;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ int table[kMfmaTable + 1];
+  __shared__ int wave_sums[kMfmaWaves];
+  __shared__ int grid_s[2];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int LP = p.L * p.P;
+
+  size_t at = 0;
+  Level* levels = reinterpret_cast<Level*>(smem + at);
+  at += sizeof(Level) * size_t(p.L);
+  LevelTiles* lt = reinterpret_cast<LevelTiles*>(smem + at);
+  at += sizeof(LevelTiles) * size_t(p.L);
+  int* order = reinterpret_cast<int*>(smem + at);
+  at += sizeof(int) * size_t(p.L);
+  int* rank_base = reinterpret_cast<int*>(smem + at);
+  at += sizeof(int) * size_t(p.L + 1);
+  at = (at + 15) & ~size_t(15);
+  int64_t* total = reinterpret_cast<int64_t*>(smem + at);  // [0]: tiles, [1]: the fetched task
+  at += 16;
+  constexpr size_t kWaveBytes = std::max(size_t(kMfmaK * 32 * NB) + 4 * size_t(kMfmaWBytes),
+                                         size_t(4 * NB * kWave * 16));
+  unsigned char* region0 = smem + at;
+  unsigned char* gst = region0 + size_t(wave) * kWaveBytes;  // grad_out rows
+  unsigned char* wt = gst + kMfmaK * 32 * NB;                // four weight tiles
+
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
+  if (ntiles <= 0 || 4 * ntiles > bg.keys_alloc) return;  // the host launches this only when bucketed
+  if (tid == 0) {
+    order_levels(p, levels, lt, order, rank_base);
+    int mx = 1, my = 1;
+    for (int i = 0; i < p.L; ++i) {
+      mx = max(mx, lt[i].ntx / 2);
+      my = max(my, lt[i].nty / 2);
+    }
+    grid_s[0] = min(mx, kMfmaMaxRegions);
+    grid_s[1] = min(my, kMfmaMaxRegions);
+  }
+  __syncthreads();
+
+  const int xcd = int(blockIdx.x) % kXcds;
+  int* queue = buckets + int64_t(p.B) * p.H * 4 * ntiles + xcd;
+  const int64_t per_tile = int64_t(p.B) * p.H;
+  const int RX = grid_s[0], RY = grid_s[1];
+  const int64_t npairs = int64_t(p.B) * RX * RY;
+  const int64_t pa = xcd * npairs / kXcds, pb = (xcd + 1) * npairs / kXcds;
+  const int64_t nentries = (pb - pa) * p.L;
+  const bool regional = nentries <= kMfmaTable;
+  int64_t queue_len = 0;
+  if (regional) {
+    // Tasks per (pair, level), then their exclusive prefix sums: four entries a thread.
+    int cnt[4], sum = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid * 4 + j;
+      cnt[j] = 0;
+      if (i < nentries) {
+        const int64_t pair = pa + i / p.L;
+        const int l = order[i % p.L];
+        const int rg = int(pair % (RX * RY)), ry = rg / RX, rx = rg - ry * RX;
+        const Level lv = levels[l];
+        const LevelTiles tl = lt[l];
+        const int nx = region_first_tile(rx + 1, RX, lv.w, tl.ntx) - region_first_tile(rx, RX, lv.w, tl.ntx);
+        const int ny = region_first_tile(ry + 1, RY, lv.h, tl.nty) - region_first_tile(ry, RY, lv.h, tl.nty);
+        cnt[j] = nx * ny * p.H;
+      }
+      sum += cnt[j];
+    }
+    int all;
+    int run = block_exclusive_scan(sum, wave_sums, &all);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = tid * 4 + j;
+      if (i <= nentries) table[i] = run;
+      run += cnt[j];
+    }
+    queue_len = all;
+  } else {
+    for (int oi = 0; oi < p.L; ++oi) {
+      const int64_t n = int64_t(rank_base[oi + 1] - rank_base[oi]) * per_tile;
+      queue_len += (xcd + 1) * n / kXcds - xcd * n / kXcds;
+    }
+  }
+  __syncthreads();
+  const int kc = lane & (kMfmaK - 1);
+  const int g16 = lane >> 4, i16 = lane & 15;
+
+  for (;;) {
+    if (tid == 0) {
+      // -1: the queue is empty. Regional: entry i and task k - table[i] in it.
+      const int64_t k = atomicAdd(queue, 1);
+      int64_t got = k < queue_len ? k : -1;
+      if (regional && got >= 0) {
+        int lo = 0, hi = int(nentries) - 1;  // the last entry whose prefix is <= k
+        while (lo < hi) {
+          const int mid = (lo + hi + 1) >> 1;
+          if (table[mid] <= k) lo = mid; else hi = mid - 1;
+        }
+        got = (int64_t(lo) << 32) | (k - table[lo]);
+      }
+      total[1] = got;
+    }
+    __syncthreads();
+    const int64_t got = total[1];
+    if (got < 0) break;  // uniform: every thread read the same value
+    int l, b, h, tile;
+    if (regional) {
+      const int i = int(got >> 32), local = int(got & 0xffffffff);
+      const int64_t pair = pa + i / p.L;
+      l = order[i % p.L];
+      b = int(pair / (RX * RY));
+      const int rg = int(pair % (RX * RY)), ry = rg / RX, rx = rg - ry * RX;
+      const Level lvr = levels[l];
+      const LevelTiles tlr = lt[l];
+      const int tx0 = region_first_tile(rx, RX, lvr.w, tlr.ntx);
+      const int nx = region_first_tile(rx + 1, RX, lvr.w, tlr.ntx) - tx0;
+      const int ty0 = region_first_tile(ry, RY, lvr.h, tlr.nty);
+      h = local % p.H;
+      const int rest = local / p.H;
+      tile = (ty0 + rest / nx) * tlr.ntx + tx0 + rest % nx;
+    } else {
+      int64_t k = got;
+      // The queue's k-th task: level order[oi], task t of that level.
+      int oi = 0;
+      int64_t tl_task = 0;
+      for (; oi < p.L; ++oi) {
+        const int64_t n = int64_t(rank_base[oi + 1] - rank_base[oi]) * per_tile;
+        const int64_t lo = xcd * n / kXcds, len = (xcd + 1) * n / kXcds - lo;
+        if (k < len) {
+          tl_task = lo + k;
+          break;
+        }
+        k -= len;
+      }
+      l = order[oi];
+      const LevelTiles tlr = lt[l];
+      const int ntl = tlr.ntx * tlr.nty;
+      h = int(tl_task % p.H);
+      const int64_t rest = tl_task / p.H;
+      tile = int(rest % ntl);
+      b = int(rest / ntl);
+    }
+    const Level lv = levels[l];
+    const LevelTiles tl = lt[l];
+    const int ty = tile / tl.ntx, tx = tile - ty * tl.ntx;
+    const int bh = b * p.H + h;
+    const uint32_t* ent = entries + int64_t(bh) * bg.region;
+    const CandRanges cr = tile_candidates(buckets + int64_t(bh) * 4 * ntiles, tl, tile, tx, ty, uint32_t(l * p.P));
+    const int64_t unit0 = int64_t(b) * p.Q * p.H + h;  // (b, q = 0, h)
+    MfmaTile t;
+    t.loc = p.loc + unit0 * LP * 2 * int64_t(sizeof(TL));
+    t.attn = p.attn + unit0 * LP * ES;
+    t.gout = p.grad_out + unit0 * D * ES;
+    t.loc_q = uint32_t(p.H * LP * 2) * uint32_t(sizeof(TL));
+    t.attn_q = uint32_t(p.H * LP * ES);
+    t.gout_q = uint32_t(p.H * D * ES);
+    t.r0 = ty << kMfmaSubLog2;
+    t.c0 = tx << kMfmaSubLog2;
+    t.r1 = min(t.r0 + (1 << kMfmaSubLog2), lv.h);
+    t.c1 = min(t.c0 + (1 << kMfmaSubLog2), lv.w);
+    t.ncand = cr.ncand;
+    t.div_lp = bg.div_lp;
+    t.LP = LP;
+
+    f32x4_v acc[4][NB];
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int j = 0; j < NB; ++j) acc[st][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+
+    // This wave's K-blocks: wave, wave + 4, ...; two register sets in turn. Block
+    // j's entries are loaded two blocks ahead and its data one block ahead, each
+    // before the loads of the block after, so that a wait for one never waits for
+    // younger loads: while block j computes, the data of j + 1 and the entries of
+    // j + 2 are in flight.
+    const uint32_t nkb = (cr.ncand + kMfmaK - 1) / kMfmaK;
+    const uint32_t mine = nkb > uint32_t(wave) ? (nkb - uint32_t(wave) + kMfmaWaves - 1) / kMfmaWaves : 0u;
+    const uint32_t step = kMfmaWaves * kMfmaK;
+    uint32_t cand = uint32_t(wave) * kMfmaK + uint32_t(kc);  // this lane's candidate in block j
+    // The main loop issues its loads unconditionally (an entry past the end reads
+    // candidate 0), so that the compiler's wait counts stay exact; the last one or
+    // two blocks run after it.
+    MfmaBlock<T, TL, NB> ba, bb;
+    uint32_t ea = 0, eb = 0, j = 0;
+    if (mine > 0) {
+      ea = cand_entry(ent, cr, cand);
+      eb = cand_entry(ent, cr, cand + step);
+      mfma_load<T, TL, NB, SOFTMAX>(t, ea, lane, ba);
+    }
+    for (; j + 2 < mine; j += 2) {
+      const uint32_t kb = uint32_t(wave) + j * kMfmaWaves;
+      const uint32_t e2 = cand_entry(ent, cr, cand + 2 * step);
+      mfma_load<T, TL, NB, SOFTMAX>(t, eb, lane, bb);
+      mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ba, lane, gst, wt, acc);
+      const uint32_t e3 = cand_entry(ent, cr, cand + 3 * step);
+      mfma_load<T, TL, NB, SOFTMAX>(t, e2, lane, ba);
+      mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb + kMfmaWaves, eb, bb, lane, gst, wt, acc);
+      ea = e2;
+      eb = e3;
+      cand += 2 * step;
+    }
+    if (j < mine) {
+      const uint32_t kb = uint32_t(wave) + j * kMfmaWaves;
+      if (j + 1 < mine) mfma_load<T, TL, NB, SOFTMAX>(t, eb, lane, bb);
+      mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ba, lane, gst, wt, acc);
+      if (j + 1 < mine) mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb + kMfmaWaves, eb, bb, lane, gst, wt, acc);
+    }
+
+    // Partial sums meet in LDS (each wave's own region, which only it used so far):
+    // wave w adds the four waves' sums of sub-tile w.
+    {
+      u32x4_v* out = reinterpret_cast<u32x4_v*>(gst);
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) out[(st * NB + nb) * kWave + lane] = __builtin_bit_cast(u32x4_v, acc[st][nb]);
+    }
+    __syncthreads();
+    f32x4_v sum[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      sum[nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int w = 0; w < kMfmaWaves; ++w)
+        sum[nb] += __builtin_bit_cast(
+            f32x4_v, reinterpret_cast<const u32x4_v*>(region0 + size_t(w) * kWaveBytes)[(wave * NB + nb) * kWave + lane]);
+    }
+    // Lane l holds C[4 g + r][16 nb + i] of sub-tile `wave`: position
+    // (r0 + 4 (wave / 2) + g, c0 + 4 (wave % 2) + r), channel 16 nb + i.
+    const int y = t.r0 + 4 * (wave >> 1) + g16;
+    if (y < t.r1) {
+      T* gv = reinterpret_cast<T*>(p.grad_value);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int x = t.c0 + 4 * (wave & 1) + r;
+        if (x < t.c1) {
+          const int64_t pos = int64_t(b) * p.S + lv.start + int64_t(y) * lv.w + x;
+          T* dst = gv + (pos * p.H + h) * D + i16;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            float v = sum[nb][r];
+            if (accumulate) v += load_acc(dst + 16 * nb);
+            store_elem(dst + 16 * nb, v);
+          }
+        }
+      }
+    }
+    __syncthreads();  // the partial sums are read before the next tile reuses the LDS
   }
 }
 
@@ -1548,7 +2110,11 @@ struct BackwardPlan {
   bool bucket;            // try the bucket sort (the kernels re-check on the device)
   size_t bucket_lds;
   int64_t bucket_chunks;  // bucketing workgroups per (b, h)
-  int64_t zero_keys;      // bucket counters to clear per (b, h)
+  int64_t zero_keys;      // bucket counters to clear per (b, h), at most
+  bool mfma;              // grad_value on the matrix cores (4 x 4 tiles)
+  int mfma_nb;            // 16-channel column blocks
+  int64_t mfma_blocks;
+  size_t mfma_lds;
   Plan sample;
 };
 
@@ -1559,6 +2125,14 @@ size_t device_lds_limit() {
       bytes <= 0)
     return 64 * 1024;
   return size_t(bytes);
+}
+
+int device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    return 256;
+  return n;
 }
 
 size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
@@ -1576,7 +2150,7 @@ size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
 
 int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, int64_t L,
                        int64_t P, int loc_dtype, const void* const* vec_ptrs, int n_vec,
-                       const void* grad_attn, size_t lds_limit, BackwardPlan* plan) {
+                       const void* grad_attn, size_t lds_limit, int cus, BackwardPlan* plan) {
   int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_vec, &plan->sample);
   if (rc != MSDA_OK) return rc;
   const int es = elem_size(dtype);
@@ -1603,17 +2177,32 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   while (owner_lds_bytes(dtype, L, D, bg.nb, bg.cap) > budget && bg.nb > 1) bg.nb >>= 1;
   if (owner_lds_bytes(dtype, L, D, bg.nb, bg.cap) > budget)
     return fail(MSDA_ERR_UNSUPPORTED, "msda: %lld levels do not fit the backward's LDS budget", (long long)L);
-  // Tiles per (b, h): every level has at most 3 h w / amin + 1 of them.
-  const int64_t tiles_bound = L + 3 * ((L * S + bg.amin - 1) / bg.amin);
-  if (tiles_bound >= (int64_t(1) << 29))
-    return fail(MSDA_ERR_UNSUPPORTED, "msda: too many backward tiles for S = %lld and L = %lld",
-                (long long)S, (long long)L);
-  bg.nw = int(std::min<int64_t>(tiles_bound, 2 * ((S + bg.cap - 1) / bg.cap) + L));
   const int64_t samples_bh = Q * L * P;
   bg.region = samples_bh;
   const int64_t attn_bytes = B * samples_bh * H * es;
   const bool attn_ok = (reinterpret_cast<uintptr_t>(grad_attn) & 3) == 0;
   bg.keys_alloc = attn_ok && samples_bh < (int64_t(1) << 32) ? attn_bytes / (4 * B * H) : 0;
+  // The matrix-core grad_value: 16-bit dtypes, D in {16, 32, 48, 64} with 16-byte
+  // aligned rows, and bucket counters for 4 x 4 tiles surely in the scratch. A level
+  // of h x w positions has ceil(h / 4) ceil(w / 4) <= h w / 4 + 1 such tiles.
+  // A level of h x w positions has ceil(h / 8) ceil(w / 8) <= h w / 8 + 1 8 x 8 tiles.
+  const int64_t mfma_tiles_bound = L * (S / 8 + 1);
+  const int64_t ls = elem_size(loc_dtype);
+  const int64_t per_image = Q * H * std::max(L * P * 2 * ls, D * es);  // 32-bit offsets inside an image
+  bool mfma_ok = (dtype == MSDA_BF16 || dtype == MSDA_F16) && D % 16 == 0 && D / 16 <= kMfmaMaxNb &&
+                 4 * mfma_tiles_bound + kXcds <= bg.keys_alloc && mfma_lds_bytes(L, D) <= lds_limit &&
+                 B * H * mfma_tiles_bound < (int64_t(1) << 31) && per_image < (int64_t(1) << 31) &&
+                 getenv("DEFORMOPS_AMD_NO_MFMA") == nullptr;
+  for (int i = 0; i < n_vec && mfma_ok; ++i) mfma_ok = aligned(vec_ptrs[i], 16);
+  plan->mfma = mfma_ok;
+  bg.sub_log2 = mfma_ok ? kMfmaSubLog2 : 0;
+  if (mfma_ok) bg.amin = 1 << (2 * kMfmaSubLog2);
+  // Tiles per (b, h): every level has at most 3 h w / amin + 1 adaptive tiles.
+  const int64_t tiles_bound = mfma_ok ? mfma_tiles_bound : L + 3 * ((L * S + bg.amin - 1) / bg.amin);
+  if (tiles_bound >= (int64_t(1) << 29))
+    return fail(MSDA_ERR_UNSUPPORTED, "msda: too many backward tiles for S = %lld and L = %lld",
+                (long long)S, (long long)L);
+  bg.nw = int(std::min<int64_t>(tiles_bound, 2 * ((S + bg.cap - 1) / bg.cap) + L));
   plan->bucket = bg.keys_alloc >= 4 * L;
   if (!plan->bucket) bg.keys_alloc = 0;
   plan->zero_keys = std::min<int64_t>(bg.keys_alloc, 4 * tiles_bound);
@@ -1625,6 +2214,18 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   plan->bucket_chunks = (samples_bh + kBucketThreads * kBucketSamples - 1) / (kBucketThreads * kBucketSamples);
   plan->owner_blocks = xcd_group_grid(H, int64_t(bg.nw) * B);
   plan->owner_lds = owner_lds_bytes(dtype, L, D, bg.nb, bg.cap);
+  plan->mfma_nb = int(D / 16);
+  plan->mfma_lds = mfma_lds_bytes(L, D);
+  if (mfma_ok) {
+    // Persistent workgroups, as many as fit the CUs at once, a multiple of 8.
+    const int64_t static_lds = sizeof(int) * (kMfmaTable + 1 + kMfmaWaves + 2);
+    const int64_t per_cu =
+        std::max<int64_t>(1, std::min<int64_t>(4, int64_t(160 * 1024) / (int64_t(plan->mfma_lds) + static_lds)));
+    const int64_t blocks = std::min<int64_t>(B * H * tiles_bound, int64_t(cus) * per_cu);
+    plan->mfma_blocks = (blocks + kXcds - 1) / kXcds * kXcds;
+  } else {
+    plan->mfma_blocks = 0;
+  }
   if (plan->owner_blocks >= 2147483647 || B * H * plan->bucket_chunks >= 2147483647 ||
       B * S >= 2147483647)
     return fail(MSDA_ERR_UNSUPPORTED, "msda: backward grid too large");
@@ -1670,16 +2271,36 @@ hipError_t launch_owner_cvr(const BackwardPlan& plan, const Problem& p, const in
   return hipErrorInvalidValue;
 }
 
+template <typename T, typename TL, bool SM>
+hipError_t launch_owner_mfma(const BackwardPlan& plan, const Problem& p, const int* buckets,
+                             const uint32_t* entries, int accumulate, hipStream_t st) {
+  if constexpr (std::is_same_v<T, bf16_t> || std::is_same_v<T, f16_t>) {
+    auto go = [&](auto k) -> hipError_t {
+      const hipError_t e = allow_lds(k, plan.mfma_lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(k, dim3(unsigned(plan.mfma_blocks)), dim3(kWave * kMfmaWaves), plan.mfma_lds, st, p,
+                         plan.bg, const_cast<int*>(buckets), entries, accumulate);
+      return hipGetLastError();
+    };
+    switch (plan.mfma_nb) {
+      case 1: return go(msda_grad_value_mfma_kernel<T, TL, 1, SM>);
+      case 2: return go(msda_grad_value_mfma_kernel<T, TL, 2, SM>);
+      case 3: return go(msda_grad_value_mfma_kernel<T, TL, 3, SM>);
+      case 4: return go(msda_grad_value_mfma_kernel<T, TL, 4, SM>);
+    }
+  }
+  return hipErrorInvalidValue;
+}
+
 // The bucket sort: clear the counters, count, scan, place.
 template <typename TL>
 hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* buckets, uint32_t* entries,
                           hipStream_t st) {
-  const int64_t clear_bytes = int64_t(p.B) * p.H * plan.zero_keys * 4;
   {
-    const int64_t chunks = clear_bytes / 16 + 1;
-    const unsigned blocks = unsigned(std::min<int64_t>((chunks + 255) / 256, 4096));
-    hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks), dim3(256), 0, st, reinterpret_cast<char*>(buckets),
-                       clear_bytes);
+    const int64_t n = int64_t(p.B) * p.H * plan.zero_keys;
+    const unsigned blocks = unsigned(std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 1024)));
+    const size_t lds = p.L > kMaxOrderedLevels ? (sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) : 0;
+    hipLaunchKernelGGL(msda_bucket_clear_kernel, dim3(blocks), dim3(256), lds, st, p, plan.bg, buckets);
   }
   const dim3 grid(unsigned(xcd_group_grid(p.H, int64_t(p.B) * plan.bucket_chunks))), block(kBucketThreads);
   auto count = msda_bucket_kernel<TL, false>;
@@ -1776,7 +2397,8 @@ int msda_launch_geometry(int value_dtype, int64_t batch, int64_t spatial, int64_
   if (backward) {
     BackwardPlan bp;
     const int rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries,
-                                      levels, points, value_dtype, nullptr, 0, nullptr, 160 * 1024, &bp);
+                                      levels, points, value_dtype, nullptr, 0, nullptr, 160 * 1024, 256,
+                                      &bp);
     if (rc != MSDA_OK) return rc;
     // The grad_value kernel's layout: channels per register item, positions per
     // tile at most, waves per workgroup and workgroups.
@@ -1881,7 +2503,8 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   const void* vec[] = {value, grad_output, grad_value};
   BackwardPlan plan;
   rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
-                          loc_dtype, vec, 3, grad_attention_weights, device_lds_limit(), &plan);
+                          loc_dtype, vec, 3, grad_attention_weights, device_lds_limit(), device_cus(),
+                          &plan);
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,
@@ -1910,8 +2533,12 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
           e = hipGetLastError();
           if (e != hipSuccess) return e;
         }
-        e = softmax ? launch_owner_cvr<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
-                    : launch_owner_cvr<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
+        if (plan.mfma)
+          e = softmax ? launch_owner_mfma<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
+                      : launch_owner_mfma<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
+        else
+          e = softmax ? launch_owner_cvr<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
+                      : launch_owner_cvr<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
         if (e != hipSuccess) return e;
         const dim3 grid(unsigned(plan.sample.num_blocks)), block(unsigned(kWave * plan.sample.waves));
         if (softmax)
