@@ -11,6 +11,7 @@ the rounded inputs; float64 1e-10.
 
 from __future__ import annotations
 
+import dataclasses
 import math
 
 import pytest
@@ -121,6 +122,7 @@ SHAPES = [
     pytest.param(((5, 5),), 1, 6, 2, 7, 2, id="d7"),
     pytest.param(((10, 12), (5, 6), (3, 3), (2, 2), (1, 1)), 2, 21, 8, 32, 4, id="five-levels"),
     pytest.param(((12, 10), (6, 5)), 1, 13, 1, 256, 2, id="d256"),
+    pytest.param(((11, 9), (6, 5), (3, 3)), 2, 19, 3, 48, 4, id="d48"),
 ]
 
 
@@ -134,6 +136,40 @@ def test_shapes_match_oracle(device, levels, B, Q, H, D, P, dtype):
     for softmax in (False, True):
         check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
                              label=f"levels={levels} B={B} Q={Q} H={H} D={D} P={P}")
+
+
+# The two grad_value kernels for 16-bit dtypes: the matrix-core one (the default for
+# D = 16, 32, 48, 64) and the VALU owner kernel (every other case, and the fallback
+# when the bucket scratch is short), selected by DEFORMOPS_AMD_NO_MFMA.
+
+
+@pytest.mark.parametrize("path", ["mfma", "valu"])
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("cfg", [2, 3])
+def test_grad_value_paths_match_oracle(device, monkeypatch, cfg, dtype, path):
+    if path == "valu":
+        monkeypatch.setenv("DEFORMOPS_AMD_NO_MFMA", "1")
+    else:
+        monkeypatch.delenv("DEFORMOPS_AMD_NO_MFMA", raising=False)
+    w = make_workload(cfg).to(device, dtype)
+    for softmax in (False, True):
+        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                             label=f"config {cfg} {path}")
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16, F32], ids=["bf16", "f16", "f32"])
+def test_samples_piled_on_one_tile(device, dtype):
+    """Every sample of every query lands near one pixel: one tile owns them all, so a
+    tile runs many K-blocks per wave and its neighbours get only straddlers."""
+    g = torch.Generator().manual_seed(9)
+    w = make_workload(0, levels=((24, 20), (12, 10)), batch=2, queries=700, heads=2, channels=32, points=4)
+    B, S, H, D, Q, L, P = w.sizes
+    centre = torch.tensor([0.41, 0.57], dtype=torch.float64)
+    loc = centre + 0.01 * torch.randn(B, Q, H, L, P, 2, generator=g, dtype=torch.float64)
+    w = dataclasses.replace(w, sampling_locations=loc.to(w.sampling_locations.dtype)).to(device, dtype)
+    for softmax in (False, True):
+        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                             label="piled")
 
 
 # Boundary semantics.
