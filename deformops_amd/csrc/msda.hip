@@ -244,6 +244,16 @@ template <typename T, int CV> struct Chan16 {
 template <int CV> struct Chan<bf16_t, CV> : Chan16<bf16_t, CV> {};
 template <int CV> struct Chan<f16_t, CV> : Chan16<f16_t, CV> {};
 
+// acc + a.lo * b.lo + a.hi * b.hi for two packed 16-bit pairs (v_dot2_f32_bf16 /
+// v_dot2_f32_f16).
+template <typename T> __device__ inline float dot2_16(uint32_t a, uint32_t b, float acc) {
+  if constexpr (__is_same(T, bf16_t))
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a), __builtin_bit_cast(bf16x2_v, b), acc,
+                                           false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_v, a), __builtin_bit_cast(f16x2_v, b), acc, false);
+}
+
 // ---------------------------------------------------------------------------
 // Cross-lane reductions inside the LH lanes of one unit (LH a power of two, the
 // unit's lanes contiguous and aligned). Every lane of the wave must call them.
@@ -442,7 +452,10 @@ __device__ inline LaneMap map_lane(const Problem& p) {
 
 // Phase 1, shared by both directions: stage every sample of the lane's unit and
 // return the unit's softmax statistics (max and 1 / sum of exp), if any.
-template <typename T, typename TL, bool SOFTMAX>
+// With PACK (16-bit value dtypes), w[0] and w[1] instead hold the bit patterns of
+// the weight pairs (w00, w01) and (w10, w11), each rounded to the value dtype, for
+// the forward's packed dot products.
+template <typename T, typename TL, bool SOFTMAX, bool PACK = false>
 __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const Level* levels,
                                      Staged<typename Elem<T>::acc>* wst,
                                      typename Elem<T>::acc& smax,
@@ -481,6 +494,12 @@ __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const L
     st.w[1] = g.w01 * a;
     st.w[2] = g.w10 * a;
     st.w[3] = g.w11 * a;
+    if constexpr (PACK) {
+      const uint32_t w01 = Chan16<T, 2>::pack(st.w[0], st.w[1]);
+      const uint32_t w23 = Chan16<T, 2>::pack(st.w[2], st.w[3]);
+      st.w[0] = __uint_as_float(w01);
+      st.w[1] = __uint_as_float(w23);
+    }
     wst[s * m.uw_count + m.uw] = st;
   }
 }
@@ -499,10 +518,15 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
   Staged<A>* wst = reinterpret_cast<Staged<A>*>(smem + sizeof(Level) * p.L) +
                    m.wave * m.uw_count * LP;
 
+  // 16-bit values: two corners per packed dot product. v_perm_b32 pairs channel i
+  // of corners (0, 1), and of (2, 3); v_dot2_f32_{bf16,f16} multiplies the pair by
+  // the staged weight pair (rounded to the value dtype) and adds to the fp32 sum:
+  // one instruction per two products, no widening.
+  constexpr bool kPacked = ES == 2 && CV >= 2;
   load_levels(p, levels);
   __syncthreads();
   A smax, sinv;
-  stage_samples<T, TL, SOFTMAX>(p, m, levels, wst, smax, sinv);
+  stage_samples<T, TL, SOFTMAX, kPacked>(p, m, levels, wst, smax, sinv);
   __syncthreads();
 
   if (!m.unit_ok || m.t * CV >= p.D) return;
@@ -511,16 +535,35 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
   A acc[CV];
 #pragma unroll
   for (int i = 0; i < CV; ++i) acc[i] = A(0);
+  if constexpr (kPacked) {
+    using R = typename Chan<T, CV>::R;
 #pragma unroll 2
-  for (int s = 0; s < LP; ++s) {
-    const Staged<A> st = wst[s * m.uw_count + m.uw];
-    A v[4][CV];
+    for (int s = 0; s < LP; ++s) {
+      const Staged<A> st = wst[s * m.uw_count + m.uw];
+      R v[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) Chan<T, CV>::load(img + (st.off[c] + lane_bytes), v[c]);
+      for (int c = 0; c < 4; ++c) v[c] = *reinterpret_cast<const R*>(img + (st.off[c] + lane_bytes));
+      const uint32_t w01 = __float_as_uint(st.w[0]), w23 = __float_as_uint(st.w[1]);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+      for (int i = 0; i < CV / 2; ++i) {
+        acc[2 * i] = dot2_16<T>(__builtin_amdgcn_perm(v[1].w[i], v[0].w[i], 0x05040100u), w01, acc[2 * i]);
+        acc[2 * i + 1] = dot2_16<T>(__builtin_amdgcn_perm(v[1].w[i], v[0].w[i], 0x07060302u), w01, acc[2 * i + 1]);
+        acc[2 * i] = dot2_16<T>(__builtin_amdgcn_perm(v[3].w[i], v[2].w[i], 0x05040100u), w23, acc[2 * i]);
+        acc[2 * i + 1] = dot2_16<T>(__builtin_amdgcn_perm(v[3].w[i], v[2].w[i], 0x07060302u), w23, acc[2 * i + 1]);
+      }
+    }
+  } else {
+#pragma unroll 2
+    for (int s = 0; s < LP; ++s) {
+      const Staged<A> st = wst[s * m.uw_count + m.uw];
+      A v[4][CV];
 #pragma unroll
-      for (int i = 0; i < CV; ++i) acc[i] = fma(st.w[c], v[c][i], acc[i]);
+      for (int c = 0; c < 4; ++c) Chan<T, CV>::load(img + (st.off[c] + lane_bytes), v[c]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int i = 0; i < CV; ++i) acc[i] = fma(st.w[c], v[c][i], acc[i]);
+    }
   }
   Chan<T, CV>::store(p.out + (m.gunit * p.D + m.t * CV) * ES, acc);
 }
@@ -579,6 +622,10 @@ constexpr int kBucketBatch = 8;     // of which loaded together
 constexpr int kTargetRecords = 8192;
 constexpr int kBucketLdsKeys = 8192;  // LDS bucket counters of the bucketing kernels (32 KB)
 constexpr int kMaxOrderedLevels = 64;
+// Scratch ints after the bucket rows for the matrix-core kernel's kXcds work-queue
+// counters, each on its own 128-byte line (plus the slack to align the first).
+constexpr int kQueueLine = 32;
+constexpr int kQueueInts = (kXcds + 1) * kQueueLine;
 
 // Unsigned 32-bit division by a divisor fixed per launch: one multiply-high, an
 // add and two shifts (Granlund and Montgomery, "Division by invariant integers
@@ -887,8 +934,8 @@ __global__ __launch_bounds__(256) void msda_bucket_clear_kernel(const Problem p,
   const int64_t ntiles = load_tiles(p, bg, levels, lt, total_s);
   const int64_t nkeys = 4 * ntiles;
   if (ntiles < 0 || nkeys > bg.keys_alloc) return;
-  // The matrix-core grad_value keeps kXcds work-queue counters right after the rows.
-  const int64_t n = int64_t(p.B) * p.H * nkeys + (bg.sub_log2 > 0 ? kXcds : 0);
+  // The matrix-core grad_value keeps its work-queue counters right after the rows.
+  const int64_t n = int64_t(p.B) * p.H * nkeys + (bg.sub_log2 > 0 ? kQueueInts : 0);
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) buckets[i] = 0;
 }
@@ -1366,9 +1413,10 @@ typedef short i16x4_v __attribute__((ext_vector_type(4)));
 
 constexpr int kMfmaWaves = 4;     // waves per workgroup, splitting a tile's K-blocks
 constexpr int kMfmaSubLog2 = 3;   // 8 x 8 position tiles of four 4 x 4 sub-tiles
-constexpr int kMfmaK = 32;        // candidates per K-block: the MFMA's K
+constexpr int kMfmaK = 64;        // candidates per K-block: one per lane, two MFMA K-steps
+constexpr int kMfmaKStep = 32;    // the MFMA's K
 constexpr int kMfmaMaxNb = 4;     // 16-channel column blocks: D <= 64
-constexpr int kMfmaWBytes = 16 * kMfmaK * 2;  // one 16 x 32 weight tile
+constexpr int kMfmaWBytes = 16 * kMfmaKStep * 2;  // one 16 x 32 weight tile
 
 template <typename T> struct MfmaOp;
 template <> struct MfmaOp<bf16_t> {
@@ -1399,13 +1447,13 @@ __device__ inline i16x4_v lds_read_tr16(const unsigned char* p) {
 // Per-wave LDS of the matrix-core kernel: the staged rows and the four weight
 // tiles during a tile, the wave's partial sums at its end.
 size_t mfma_wave_bytes(int64_t D) {
-  const size_t work = size_t(kMfmaK) * size_t(2 * D) + 4 * size_t(kMfmaWBytes);
+  const size_t work = size_t(kMfmaK) * size_t(2 * D) + 4 * size_t(kMfmaWBytes);  // rows + 4 weight tiles
   const size_t partial = 4 * size_t(D / 16) * kWave * 16;
   return std::max(work, partial);
 }
 
 size_t mfma_head_bytes(int64_t L) {
-  size_t at = (sizeof(Level) + sizeof(LevelTiles) + sizeof(int)) * size_t(L) + sizeof(int) * size_t(L + 1);
+  size_t at = (sizeof(Level) + sizeof(LevelTiles) + 2 * sizeof(int)) * size_t(L) + sizeof(int) * size_t(L + 1);
   at = (at + 15) & ~size_t(15);
   return at + 16;
 }
@@ -1466,11 +1514,11 @@ __device__ inline uint32_t cand_entry(const uint32_t* __restrict__ ent, const Ca
 }
 
 // One K-block's loads for one lane: its candidate's location and weight, and its
-// share of the block's grad_out rows (flat 16-byte piece lane + 64 j of 32 rows).
+// share of the block's grad_out rows (flat 16-byte piece lane + 64 j of 64 rows).
 template <typename T, typename TL, int NB> struct MfmaBlock {
   LocPair<TL> loc;
   T attn;
-  u32x4_v piece[NB];
+  u32x4_v piece[2 * NB];
 };
 
 // Per-tile constants of the matrix-core kernel (all wave-uniform).
@@ -1492,14 +1540,16 @@ __device__ inline void mfma_load(const MfmaTile& t, uint32_t e, int lane, MfmaBl
   d.loc = *reinterpret_cast<const LocPair<TL>*>(t.loc + (q * t.loc_q + s * uint32_t(2 * sizeof(TL))));
   if constexpr (!SOFTMAX) d.attn = *reinterpret_cast<const T*>(t.attn + (q * t.attn_q + s * 2u));
 #pragma unroll
-  for (int j = 0; j < NB; ++j) {
+  for (int j = 0; j < 2 * NB; ++j) {
     const int f = lane + kWave * j, row = f / kPieces, pc = f - row * kPieces;
     const uint32_t qr = uint32_t(__shfl(int(q), row));
     d.piece[j] = *reinterpret_cast<const u32x4_v*>(t.gout + (qr * t.gout_q + uint32_t(pc * 16)));
   }
 }
 
-// One K-block of one wave: stage, scatter the weights, four sub-tiles of MFMAs.
+// One K-block of one wave: stage the 64 grad_out rows, then per MFMA K-step (the
+// candidates of lanes 0-31, then 32-63) scatter their corner weights into the four
+// zeroed weight tiles and run the four sub-tiles' MFMAs.
 template <typename T, typename TL, int NB, bool SOFTMAX>
 __device__ inline void mfma_kblock(const MfmaTile& t, const Level& lv, uint32_t kb, uint32_t e,
                                    const MfmaBlock<T, TL, NB>& d, int lane, unsigned char* gst,
@@ -1508,13 +1558,13 @@ __device__ inline void mfma_kblock(const MfmaTile& t, const Level& lv, uint32_t 
   using V = typename Op::V;
   constexpr int kRowBytes = 32 * NB;
   constexpr int kPieces = NB * 2;
-  const int kc = lane & (kMfmaK - 1), half = lane >> 5;
+  const int kc = lane & (kMfmaKStep - 1), half = lane >> 5;
   const int g16 = lane >> 4, i16 = lane & 15;
-  const uint32_t c = kb * kMfmaK + uint32_t(kc);
-  // This lane's two corners: row `half` of the sample's 2 x 2 footprint, as LDS byte
-  // offsets of their weights (-1: not in the tile).
-  int o0 = -1, o1 = -1;
-  float w0 = 0.f, w1 = 0.f;
+  const uint32_t c = kb * kMfmaK + uint32_t(lane);
+  // The candidate's four corners as LDS byte offsets of their weights in the tiles
+  // (-1: not in the tile).
+  int o[4] = {-1, -1, -1, -1};
+  float w[4] = {0.f, 0.f, 0.f, 0.f};
   if (c < t.ncand) {
     const Geom<float> g = geometry<float>(to_acc(d.loc.x), to_acc(d.loc.y), lv, 0u, 1u);
     float a;
@@ -1524,56 +1574,79 @@ __device__ inline void mfma_kblock(const MfmaTile& t, const Level& lv, uint32_t 
     } else {
       a = to_acc(d.attn);
     }
-    const int y = g.iy + half - t.r0;
-    const bool row_in = y >= 0 && g.iy + half < t.r1;
-    const bool ma = half ? g.m10 : g.m00, mb = half ? g.m11 : g.m01;
-    const float wa = half ? g.w10 : g.w00, wb = half ? g.w11 : g.w01;
-    const int x0 = g.ix - t.c0;
-    // Position (y, x) of the tile: sub-tile (y / 4) * 2 + x / 4, row (y % 4) * 4 + x % 4.
-    const int ybase = (y >> 2) * 2 * kMfmaWBytes + (y & 3) * 4 * (2 * kMfmaK) + kc * 2;
-    if (row_in && ma && x0 >= 0 && g.ix < t.c1) {
-      o0 = ybase + (x0 >> 2) * kMfmaWBytes + (x0 & 3) * (2 * kMfmaK);
-      w0 = wa * a;
-    }
-    const int x1 = x0 + 1;
-    if (row_in && mb && x1 >= 0 && g.ix + 1 < t.c1) {
-      o1 = ybase + (x1 >> 2) * kMfmaWBytes + (x1 & 3) * (2 * kMfmaK);
-      w1 = wb * a;
+    const bool m[4] = {g.m00, g.m01, g.m10, g.m11};
+    const float wb[4] = {g.w00, g.w01, g.w10, g.w11};
+    const int y0 = g.iy - t.r0, x0 = g.ix - t.c0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int y = y0 + (k >> 1), x = x0 + (k & 1);
+      // Position (y, x) of the tile: sub-tile (y / 4) * 2 + x / 4, row (y % 4) * 4 + x % 4.
+      if (m[k] && y >= 0 && x >= 0 && t.r0 + y < t.r1 && t.c0 + x < t.c1) {
+        o[k] = ((y >> 2) * 2 + (x >> 2)) * kMfmaWBytes + ((y & 3) * 4 + (x & 3)) * (2 * kMfmaKStep) + kc * 2;
+        w[k] = wb[k] * a;
+      }
     }
   }
+  uint16_t wr[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) wr[k] = Op::round(w[k]);
   wave_lds_order();  // after the previous K-block's operand reads
   const u32x4_v zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int st = 0; st < 4; ++st) *reinterpret_cast<u32x4_v*>(wt + st * kMfmaWBytes + lane * 16) = zero;
-#pragma unroll
-  for (int j = 0; j < NB; ++j) {
+  for (int j = 0; j < 2 * NB; ++j) {
     const int f = lane + kWave * j, row = f / kPieces;
     const bool ok = kb * kMfmaK + uint32_t(row) < t.ncand;  // past the end: zero rows
     *reinterpret_cast<u32x4_v*>(gst + f * 16) = ok ? d.piece[j] : zero;
   }
-  wave_lds_order();
-  if (o0 >= 0) *reinterpret_cast<uint16_t*>(wt + o0) = Op::round(w0);
-  if (o1 >= 0) *reinterpret_cast<uint16_t*>(wt + o1) = Op::round(w1);
-  wave_lds_order();
-  V bv[NB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const unsigned char* src = gst + (8 * g16 + i16 / 4) * kRowBytes + (16 * nb + 4 * (i16 & 3)) * 2;
-    const i16x4_v t0 = lds_read_tr16(src);
-    const i16x4_v t1 = lds_read_tr16(src + 4 * kRowBytes);
-    bv[nb] = __builtin_bit_cast(V, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7));
-  }
-  const int aoff = i16 * (2 * kMfmaK) + g16 * 16;
+  for (int ks = 0; ks < 2; ++ks) {
+    wave_lds_order();
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    const V av = __builtin_bit_cast(V, *reinterpret_cast<const u32x4_v*>(wt + st * kMfmaWBytes + aoff));
+    for (int st = 0; st < 4; ++st) *reinterpret_cast<u32x4_v*>(wt + st * kMfmaWBytes + lane * 16) = zero;
+    wave_lds_order();
+    if (half == ks) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[st][nb] = Op::mma(av, bv[nb], acc[st][nb]);
+      for (int k = 0; k < 4; ++k)
+        if (o[k] >= 0) *reinterpret_cast<uint16_t*>(wt + o[k]) = wr[k];
+    }
+    wave_lds_order();
+    V bv[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const unsigned char* src =
+          gst + (kMfmaKStep * ks + 8 * g16 + i16 / 4) * kRowBytes + (16 * nb + 4 * (i16 & 3)) * 2;
+      const i16x4_v t0 = lds_read_tr16(src);
+      const i16x4_v t1 = lds_read_tr16(src + 4 * kRowBytes);
+      bv[nb] = __builtin_bit_cast(V, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7));
+    }
+    const int aoff = i16 * (2 * kMfmaKStep) + g16 * 16;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const V av = __builtin_bit_cast(V, *reinterpret_cast<const u32x4_v*>(wt + st * kMfmaWBytes + aoff));
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[st][nb] = Op::mma(av, bv[nb], acc[st][nb]);
+    }
   }
 }
 
+// Workgroups per CU the register budget of the matrix-core kernel allows.
+constexpr int mfma_blocks_per_cu(int nb) { return nb == 1 ? 4 : nb == 2 ? 3 : 2; }
+
 constexpr int kMfmaMaxRegions = 16;  // regions per axis at most
 constexpr int kMfmaTable = 1024;      // entries of a queue's prefix table at most
+constexpr int kMfmaMaxChunk = 8;      // tasks a workgroup takes from its queue at once, at most
+
+// Region (x, y) of Morton (Z-order) index z: x takes the even bits, y the odd ones,
+// so consecutive indices stay in compact 2D blocks.
+__device__ inline void morton_decode(int z, int* x, int* y) {
+  int rx = 0, ry = 0;
+  for (int bit = 0; bit < 8; ++bit) {
+    rx |= ((z >> (2 * bit)) & 1) << bit;
+    ry |= ((z >> (2 * bit + 1)) & 1) << bit;
+  }
+  *x = rx;
+  *y = ry;
+}
 
 // The first tile column (or row) of region r of n regions across a level `extent`
 // positions wide with `ntiles` tiles: tile t, centred at position S t + S / 2 (S =
@@ -1589,24 +1662,26 @@ __device__ inline int region_first_tile(int r, int n, int extent, int ntiles) {
 
 // Work distribution: a persistent grid with one work queue per XCD (a counter in
 // the scratch after the bucket counters; workgroup w serves queue w % 8, the XCD the
-// dispatcher deals it to). The image is cut into RX x RY regions in normalized
+// dispatcher deals it to). The image is cut into R x R regions in normalized
 // coordinates, and a tile of any level belongs to the region of its centre: the
 // tiles of one region at all levels gather nearly the same queries, because a
 // query samples every level at the same normalized place. Queue x holds the x-th
-// eighth of the (b, region) pairs; per pair the tasks (tile, h) run level by level,
+// eighth of the (b, region) pairs, regions in Morton order; per pair the tasks
+// (tile, h) run level by level,
 // heaviest tiles first, heads fastest. So an XCD's workgroups share one compact
 // neighbourhood of queries in their L2 at a time, and a workgroup that finishes
 // early takes the next task of its queue. A small LDS table of prefix counts per
 // (pair, level) maps a queue position to its task. When the table would not fit,
 // queue x holds the x-th eighth of each level's tasks (b, tile, h) in raster order.
 template <typename T, typename TL, int NB, bool SOFTMAX>
-__global__ __launch_bounds__(kWave * kMfmaWaves, NB <= 2 ? 4 : 2) void msda_grad_value_mfma_kernel(
+__global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void msda_grad_value_mfma_kernel(
     const Problem p, const BwdGeom bg, int* __restrict__ buckets,
     const uint32_t* __restrict__ entries, const int accumulate) {
   constexpr int D = 16 * NB;
   constexpr int ES = 2;
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int table[kMfmaTable + 1];
+  __shared__ int table[kMfmaTable + 1];  // per (pair, level): prefix count of chunks
+  __shared__ int ntab[kMfmaTable];       // per (pair, level): tasks
   __shared__ int wave_sums[kMfmaWaves];
   __shared__ int grid_s[2];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -1621,6 +1696,8 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, NB <= 2 ? 4 : 2) void msda_grad
   at += sizeof(int) * size_t(p.L);
   int* rank_base = reinterpret_cast<int*>(smem + at);
   at += sizeof(int) * size_t(p.L + 1);
+  int* csz = reinterpret_cast<int*>(smem + at);  // tasks per chunk of each ordered level
+  at += sizeof(int) * size_t(p.L);
   at = (at + 15) & ~size_t(15);
   int64_t* total = reinterpret_cast<int64_t*>(smem + at);  // [0]: tiles, [1]: the fetched task
   at += 16;
@@ -1634,27 +1711,40 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, NB <= 2 ? 4 : 2) void msda_grad
   if (ntiles <= 0 || 4 * ntiles > bg.keys_alloc) return;  // the host launches this only when bucketed
   if (tid == 0) {
     order_levels(p, levels, lt, order, rank_base);
-    int mx = 1, my = 1;
+    // R x R regions, R the power of two nearest the finest level's tile count, at most 16.
+    int mt = 1;
+    for (int i = 0; i < p.L; ++i) mt = max(mt, max(lt[i].ntx, lt[i].nty));
+    int r = 1;
+    while (r < kMfmaMaxRegions && 2 * r <= mt) r *= 2;
+    grid_s[0] = r;
+    // A tile's expected work goes as 1 / (level area): chunks of the smallest level
+    // hold one task, a level k times larger min(k, kMfmaMaxChunk) tasks.
+    int64_t amin = 0;
     for (int i = 0; i < p.L; ++i) {
-      mx = max(mx, lt[i].ntx / 2);
-      my = max(my, lt[i].nty / 2);
+      const int64_t area = int64_t(levels[i].h) * levels[i].w;
+      if (levels[i].ok && (amin == 0 || area < amin)) amin = area;
     }
-    grid_s[0] = min(mx, kMfmaMaxRegions);
-    grid_s[1] = min(my, kMfmaMaxRegions);
+    for (int i = 0; i < p.L; ++i) {
+      const int64_t area = int64_t(levels[order[i]].h) * levels[order[i]].w;
+      csz[i] = int(amin > 0 ? std::max<int64_t>(1, std::min<int64_t>(kMfmaMaxChunk, area / amin)) : 1);
+    }
   }
   __syncthreads();
 
   const int xcd = int(blockIdx.x) % kXcds;
-  int* queue = buckets + int64_t(p.B) * p.H * 4 * ntiles + xcd;
+  int* queue = reinterpret_cast<int*>(
+                   (reinterpret_cast<uintptr_t>(buckets + int64_t(p.B) * p.H * 4 * ntiles) + 4 * kQueueLine - 1) &
+                   ~uintptr_t(4 * kQueueLine - 1)) +
+               xcd * kQueueLine;
   const int64_t per_tile = int64_t(p.B) * p.H;
-  const int RX = grid_s[0], RY = grid_s[1];
-  const int64_t npairs = int64_t(p.B) * RX * RY;
+  const int R = grid_s[0];  // regions per axis, a power of two; visited in Morton order
+  const int64_t npairs = int64_t(p.B) * R * R;
   const int64_t pa = xcd * npairs / kXcds, pb = (xcd + 1) * npairs / kXcds;
   const int64_t nentries = (pb - pa) * p.L;
   const bool regional = nentries <= kMfmaTable;
   int64_t queue_len = 0;
   if (regional) {
-    // Tasks per (pair, level), then their exclusive prefix sums: four entries a thread.
+    // Chunks per (pair, level), then their exclusive prefix sums: four entries a thread.
     int cnt[4], sum = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1663,12 +1753,14 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, NB <= 2 ? 4 : 2) void msda_grad
       if (i < nentries) {
         const int64_t pair = pa + i / p.L;
         const int l = order[i % p.L];
-        const int rg = int(pair % (RX * RY)), ry = rg / RX, rx = rg - ry * RX;
+        int rx, ry;
+        morton_decode(int(pair % (R * R)), &rx, &ry);
         const Level lv = levels[l];
         const LevelTiles tl = lt[l];
-        const int nx = region_first_tile(rx + 1, RX, lv.w, tl.ntx) - region_first_tile(rx, RX, lv.w, tl.ntx);
-        const int ny = region_first_tile(ry + 1, RY, lv.h, tl.nty) - region_first_tile(ry, RY, lv.h, tl.nty);
-        cnt[j] = nx * ny * p.H;
+        const int nx = region_first_tile(rx + 1, R, lv.w, tl.ntx) - region_first_tile(rx, R, lv.w, tl.ntx);
+        const int ny = region_first_tile(ry + 1, R, lv.h, tl.nty) - region_first_tile(ry, R, lv.h, tl.nty);
+        ntab[i] = nx * ny * p.H;
+        cnt[j] = (ntab[i] + csz[i % p.L] - 1) / csz[i % p.L];
       }
       sum += cnt[j];
     }
@@ -1688,21 +1780,35 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, NB <= 2 ? 4 : 2) void msda_grad
     }
   }
   __syncthreads();
-  const int kc = lane & (kMfmaK - 1);
   const int g16 = lane >> 4, i16 = lane & 15;
 
+  // Thread 0: the rest of the current chunk, tasks [cur_local, cur_end) of entry cur_i.
+  int cur_i = 0, cur_local = 0, cur_end = 0;
   for (;;) {
     if (tid == 0) {
-      // -1: the queue is empty. Regional: entry i and task k - table[i] in it.
-      const int64_t k = atomicAdd(queue, 1);
-      int64_t got = k < queue_len ? k : -1;
-      if (regional && got >= 0) {
-        int lo = 0, hi = int(nentries) - 1;  // the last entry whose prefix is <= k
-        while (lo < hi) {
-          const int mid = (lo + hi + 1) >> 1;
-          if (table[mid] <= k) lo = mid; else hi = mid - 1;
+      // -1: the queue is empty. Regional: entry i and task `local` in it; a chunk's
+      // tasks are queue neighbours and share their queries' cache lines.
+      int64_t got = -1;
+      if (regional) {
+        if (cur_local >= cur_end) {
+          const int64_t c = atomicAdd(queue, 1);
+          cur_i = -1;
+          if (c < queue_len) {
+            int lo = 0, hi = int(nentries) - 1;  // the last entry whose prefix is <= c
+            while (lo < hi) {
+              const int mid = (lo + hi + 1) >> 1;
+              if (table[mid] <= c) lo = mid; else hi = mid - 1;
+            }
+            const int cs = csz[lo % p.L];
+            cur_i = lo;
+            cur_local = int(c - table[lo]) * cs;
+            cur_end = min(cur_local + cs, ntab[lo]);
+          }
         }
-        got = (int64_t(lo) << 32) | (k - table[lo]);
+        if (cur_i >= 0) got = (int64_t(cur_i) << 32) | cur_local++;
+      } else {
+        const int64_t k = atomicAdd(queue, 1);
+        got = k < queue_len ? k : -1;
       }
       total[1] = got;
     }
@@ -1714,13 +1820,14 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, NB <= 2 ? 4 : 2) void msda_grad
       const int i = int(got >> 32), local = int(got & 0xffffffff);
       const int64_t pair = pa + i / p.L;
       l = order[i % p.L];
-      b = int(pair / (RX * RY));
-      const int rg = int(pair % (RX * RY)), ry = rg / RX, rx = rg - ry * RX;
+      b = int(pair / (R * R));
+      int rx, ry;
+      morton_decode(int(pair % (R * R)), &rx, &ry);
       const Level lvr = levels[l];
       const LevelTiles tlr = lt[l];
-      const int tx0 = region_first_tile(rx, RX, lvr.w, tlr.ntx);
-      const int nx = region_first_tile(rx + 1, RX, lvr.w, tlr.ntx) - tx0;
-      const int ty0 = region_first_tile(ry, RY, lvr.h, tlr.nty);
+      const int tx0 = region_first_tile(rx, R, lvr.w, tlr.ntx);
+      const int nx = region_first_tile(rx + 1, R, lvr.w, tlr.ntx) - tx0;
+      const int ty0 = region_first_tile(ry, R, lvr.h, tlr.nty);
       h = local % p.H;
       const int rest = local / p.H;
       tile = (ty0 + rest / nx) * tlr.ntx + tx0 + rest % nx;
@@ -1782,7 +1889,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, NB <= 2 ? 4 : 2) void msda_grad
     const uint32_t nkb = (cr.ncand + kMfmaK - 1) / kMfmaK;
     const uint32_t mine = nkb > uint32_t(wave) ? (nkb - uint32_t(wave) + kMfmaWaves - 1) / kMfmaWaves : 0u;
     const uint32_t step = kMfmaWaves * kMfmaK;
-    uint32_t cand = uint32_t(wave) * kMfmaK + uint32_t(kc);  // this lane's candidate in block j
+    uint32_t cand = uint32_t(wave) * kMfmaK + uint32_t(lane);  // this lane's candidate in block j
     // The main loop issues its loads unconditionally (an entry past the end reads
     // candidate 0), so that the compiler's wait counts stay exact; the last one or
     // two blocks run after it.
@@ -2190,7 +2297,7 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   const int64_t ls = elem_size(loc_dtype);
   const int64_t per_image = Q * H * std::max(L * P * 2 * ls, D * es);  // 32-bit offsets inside an image
   bool mfma_ok = (dtype == MSDA_BF16 || dtype == MSDA_F16) && D % 16 == 0 && D / 16 <= kMfmaMaxNb &&
-                 4 * mfma_tiles_bound + kXcds <= bg.keys_alloc && mfma_lds_bytes(L, D) <= lds_limit &&
+                 4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc && mfma_lds_bytes(L, D) <= lds_limit &&
                  B * H * mfma_tiles_bound < (int64_t(1) << 31) && per_image < (int64_t(1) << 31) &&
                  getenv("DEFORMOPS_AMD_NO_MFMA") == nullptr;
   for (int i = 0; i < n_vec && mfma_ok; ++i) mfma_ok = aligned(vec_ptrs[i], 16);
@@ -2218,9 +2325,10 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   plan->mfma_lds = mfma_lds_bytes(L, D);
   if (mfma_ok) {
     // Persistent workgroups, as many as fit the CUs at once, a multiple of 8.
-    const int64_t static_lds = sizeof(int) * (kMfmaTable + 1 + kMfmaWaves + 2);
+    const int64_t static_lds = sizeof(int) * (2 * kMfmaTable + 1 + kMfmaWaves + 2);
     const int64_t per_cu =
-        std::max<int64_t>(1, std::min<int64_t>(4, int64_t(160 * 1024) / (int64_t(plan->mfma_lds) + static_lds)));
+        std::max<int64_t>(1, std::min<int64_t>(mfma_blocks_per_cu(int(D / 16)),
+                                               int64_t(160 * 1024) / (int64_t(plan->mfma_lds) + static_lds)));
     const int64_t blocks = std::min<int64_t>(B * H * tiles_bound, int64_t(cus) * per_cu);
     plan->mfma_blocks = (blocks + kXcds - 1) / kXcds * kXcds;
   } else {
