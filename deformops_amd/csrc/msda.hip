@@ -69,6 +69,8 @@ template <> struct Elem<f16_t> { using acc = float; static constexpr int size = 
 
 typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
 
 __device__ inline float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ inline float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -664,6 +666,11 @@ struct BwdGeom {
   FastDiv div_lp;   // by L * P
   FastDiv div_p;    // by P
   int sub_log2;     // > 0: every tile is 2^sub_log2 square (the matrix-core grad_value)
+  int group4;       // samples go in groups of 4 of one query and level (L P and P multiples of 4)
+  FastDiv div_gpq;  // by L * P / 4, groups per query
+  FastDiv div_gpl;  // by P / 4, groups per level
+  int key_bytes;    // 2 or 4: the count pass saves every sample's key in the grad_value
+                    // scratch for the place pass; 0: the place pass recomputes them
 };
 
 struct LevelTiles {
@@ -894,6 +901,182 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket_kernel(const Probl
   }
 }
 
+// The bucket key of a sample at level lv (-1: out of range), with the same pixel
+// map as the kernels that own the tiles.
+template <typename A>
+__device__ inline int sample_key(A lx, A ly, const Level& lv, const LevelTiles& t) {
+#pragma clang fp contract(off)
+  const A x = lx * A(lv.w) - A(0.5);
+  const A y = ly * A(lv.h) - A(0.5);
+  const bool in = lv.ok && x >= A(-1) && x < A(lv.w) && y >= A(-1) && y < A(lv.h);
+  return in ? bucket_key(t, int(floor(x)), int(floor(y)), lv) : -1;
+}
+
+template <int N> struct KeyWord;
+template <> struct KeyWord<2> { using type = u32x2_v; };  // four 16-bit keys
+template <> struct KeyWord<4> { using type = u32x4_v; };  // four 32-bit keys
+
+// The bucketing passes for groups of 4 consecutive samples (q, s .. s + 3) of one
+// query and level (L * P and P multiples of 4): one 16- or 32-byte location load and
+// one query / level decode per group. Workgroup: kBucketThreads * kBucketSamples
+// consecutive samples of one (b, h), thread t taking groups t, t + 256, ...
+// The count pass publishes per-bucket counts as msda_bucket_kernel does and saves
+// the four keys (16-bit when the keys fit, 0xffff / -1 for out of range) in the
+// grad_value scratch, which nothing else uses before the sort ends; the place pass
+// reads them back and hands out slots.
+template <typename TL, bool PLACE, int KB>
+__global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Problem p, const BwdGeom bg,
+                                                                      int* __restrict__ buckets,
+                                                                      uint32_t* __restrict__ entries,
+                                                                      int chunks_per_bh) {
+  using A = typename Elem<TL>::acc;
+  using Word = typename KeyWord<KB>::type;
+  constexpr int kGroups = kBucketSamples / 4;  // groups per thread
+  extern __shared__ __align__(16) unsigned char smem[];
+  Level* levels = reinterpret_cast<Level*>(smem);
+  LevelTiles* lt = reinterpret_cast<LevelTiles*>(smem + sizeof(Level) * size_t(p.L));
+  const size_t head = ((sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) + 15) & ~size_t(15);
+  int64_t* total = reinterpret_cast<int64_t*>(smem + head);
+  int* hist = reinterpret_cast<int*>(smem + head + 16);
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
+  const int64_t nkeys = 4 * ntiles;
+  if (ntiles < 0 || nkeys > bg.keys_alloc) return;  // no bucketing: the owners scan
+  const bool in_lds = nkeys <= bg.keys_lds;
+  int group, h;
+  if (!xcd_group_block(p.H, p.B * chunks_per_bh, &group, &h)) return;
+  const int chunk = group % chunks_per_bh;
+  const int b = group / chunks_per_bh;
+  const int bh = b * p.H + h;
+  const int LP = p.L * p.P;
+  const int64_t nsamples = int64_t(p.Q) * LP;
+  int* bucket_row = buckets + int64_t(bh) * nkeys;
+  uint32_t* out = entries + int64_t(bh) * bg.region;
+  Word* keys = reinterpret_cast<Word*>(p.grad_value) + int64_t(bh) * (bg.region / 4);
+  const int64_t g0 = int64_t(chunk) * kBucketThreads * kGroups;  // first group of the chunk
+  const int64_t ngroups = nsamples / 4;
+  const uint32_t gpq = uint32_t(LP / 4);  // groups per query
+  const char* loc_bh = reinterpret_cast<const char*>(p.loc) + (int64_t(b) * p.Q * p.H + h) * LP * 2 * int64_t(sizeof(TL));
+  const uint32_t loc_q = uint32_t(p.H * LP * 2) * uint32_t(sizeof(TL));  // bytes per query
+
+  // The four keys of group g (all -1 past the end).
+  auto keys_of = [&](int64_t g, int (&k)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = -1;
+    if (g >= ngroups) return;
+    const uint32_t g32 = uint32_t(g);
+    const uint32_t q = fdiv(g32, bg.div_gpq), r = g32 - q * gpq;
+    const int l = int(fdiv(r, bg.div_gpl));
+    const char* lc = loc_bh + (q * loc_q + r * uint32_t(8 * sizeof(TL)));
+    A xy[8];
+    if constexpr (sizeof(TL) == 2) {
+      const u32x4_v w = *reinterpret_cast<const u32x4_v*>(lc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        xy[2 * i] = Chan16<TL, 2>::lo(w[i]);
+        xy[2 * i + 1] = Chan16<TL, 2>::hi(w[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) xy[i] = load_acc(reinterpret_cast<const TL*>(lc) + i);
+    }
+    const Level lv = levels[l];
+    const LevelTiles tl = lt[l];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = sample_key<A>(xy[2 * i], xy[2 * i + 1], lv, tl);
+  };
+  auto save = [&](int64_t g, const int (&k)[4]) __attribute__((always_inline)) {
+    if (g >= ngroups) return;
+    Word w;
+    if constexpr (KB == 2) {
+      w[0] = (uint32_t(k[0]) & 0xffffu) | (uint32_t(k[1]) << 16);
+      w[1] = (uint32_t(k[2]) & 0xffffu) | (uint32_t(k[3]) << 16);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) w[i] = uint32_t(k[i]);
+    }
+    keys[g] = w;
+  };
+  auto restore = [&](int64_t g, int (&k)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = -1;
+    if (g >= ngroups) return;
+    const Word w = keys[g];
+    if constexpr (KB == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t v = (w[i >> 1] >> (16 * (i & 1))) & 0xffffu;
+        k[i] = v == 0xffffu ? -1 : int(v);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) k[i] = int(w[i]);
+    }
+  };
+
+  if (!in_lds) {
+    // Too many buckets for LDS: one global atomic per sample.
+    for (int i = 0; i < kGroups; ++i) {
+      const int64_t g = g0 + int64_t(i) * kBucketThreads + threadIdx.x;
+      int key[4];
+      if constexpr (PLACE) {
+        restore(g, key);
+      } else {
+        keys_of(g, key);
+        save(g, key);
+      }
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (key[c] < 0) continue;
+        const int at = atomicAdd(&bucket_row[key[c]], 1);
+        if constexpr (PLACE) out[at] = uint32_t(4 * g + c);
+      }
+    }
+    return;
+  }
+  for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) hist[k] = 0;
+  __syncthreads();
+  if constexpr (!PLACE) {
+#pragma unroll 2
+    for (int i = 0; i < kGroups; ++i) {
+      const int64_t g = g0 + int64_t(i) * kBucketThreads + threadIdx.x;
+      int key[4];
+      keys_of(g, key);
+      save(g, key);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (key[c] >= 0) atomicAdd(&hist[key[c]], 1);
+    }
+    __syncthreads();
+    for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) {
+      const int c = hist[k];
+      if (c > 0) atomicAdd(&bucket_row[k], c);
+    }
+  } else {
+    // Counts again (from the saved keys), then this workgroup's range of every bucket.
+    int key[kGroups][4];
+#pragma unroll
+    for (int i = 0; i < kGroups; ++i) {
+      restore(g0 + int64_t(i) * kBucketThreads + threadIdx.x, key[i]);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (key[i][c] >= 0) atomicAdd(&hist[key[i][c]], 1);
+    }
+    __syncthreads();
+    for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) {
+      const int c = hist[k];
+      if (c > 0) hist[k] = atomicAdd(&bucket_row[k], c);  // this workgroup's cursor in bucket k
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kGroups; ++i) {
+      const int64_t g = g0 + int64_t(i) * kBucketThreads + threadIdx.x;
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (key[i][c] >= 0) out[atomicAdd(&hist[key[i][c]], 1)] = uint32_t(4 * g + c);
+    }
+  }
+}
+
 // Counts to exclusive offsets, one workgroup per (b, h).
 __global__ __launch_bounds__(1024) void msda_bucket_scan_kernel(const Problem p, const BwdGeom bg,
                                                                 int* __restrict__ buckets) {
@@ -978,8 +1161,6 @@ template <typename TL> struct LocPair {
 
 // One grad_out piece of CVR channels as a native vector type, so that arrays of
 // them stay in VGPRs across the batch loop.
-typedef uint32_t u32x2_v __attribute__((ext_vector_type(2)));
-typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
 template <int BYTES> struct PieceOf;
 template <> struct PieceOf<2> { using type = uint16_t; };
 template <> struct PieceOf<4> { using type = uint32_t; };
@@ -2258,7 +2439,9 @@ size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
 int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, int64_t L,
                        int64_t P, int loc_dtype, const void* const* vec_ptrs, int n_vec,
                        const void* grad_attn, size_t lds_limit, int cus, BackwardPlan* plan) {
-  int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_vec, &plan->sample);
+  // vec_ptrs: value, grad_output, grad_value (channel vectors), then the locations.
+  const int n_chan = std::min(n_vec, 3);
+  int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_chan, &plan->sample);
   if (rc != MSDA_OK) return rc;
   const int es = elem_size(dtype);
   // Channels per register item: the widest power of two that divides D, fits a
@@ -2266,7 +2449,7 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   int cvr = 16 / es;
   while (cvr > 1) {
     bool ok = D % cvr == 0;
-    for (int i = 0; i < n_vec && ok; ++i) ok = aligned(vec_ptrs[i], cvr * es);
+    for (int i = 0; i < n_chan && ok; ++i) ok = aligned(vec_ptrs[i], cvr * es);
     if (ok) break;
     cvr >>= 1;
   }
@@ -2300,7 +2483,7 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
                  4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc && mfma_lds_bytes(L, D) <= lds_limit &&
                  B * H * mfma_tiles_bound < (int64_t(1) << 31) && per_image < (int64_t(1) << 31) &&
                  getenv("DEFORMOPS_AMD_NO_MFMA") == nullptr;
-  for (int i = 0; i < n_vec && mfma_ok; ++i) mfma_ok = aligned(vec_ptrs[i], 16);
+  for (int i = 0; i < n_chan && mfma_ok; ++i) mfma_ok = aligned(vec_ptrs[i], 16);
   plan->mfma = mfma_ok;
   bg.sub_log2 = mfma_ok ? kMfmaSubLog2 : 0;
   if (mfma_ok) bg.amin = 1 << (2 * kMfmaSubLog2);
@@ -2339,6 +2522,17 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
     return fail(MSDA_ERR_UNSUPPORTED, "msda: backward grid too large");
   bg.div_lp = make_fastdiv(uint32_t(L * P));
   bg.div_p = make_fastdiv(uint32_t(P));
+  // Grouped bucketing: groups of 4 samples, LDS counters for every bucket, and the
+  // saved keys (16-bit when every key fits) inside grad_value.
+  const void* loc_ptr = n_vec > 3 ? vec_ptrs[3] : nullptr;
+  bg.group4 = (L * P) % 4 == 0 && P % 4 == 0 && plan->bucket && (loc_ptr == nullptr || aligned(loc_ptr, 16));
+  bg.key_bytes = 4 * tiles_bound < 0xffff ? 2 : 4;
+  if (B * H * samples_bh * bg.key_bytes > B * S * H * D * es) bg.group4 = 0;
+  if (!bg.group4) bg.key_bytes = 0;
+  if (bg.group4) {
+    bg.div_gpq = make_fastdiv(uint32_t(L * P / 4));
+    bg.div_gpl = make_fastdiv(uint32_t(P / 4));
+  }
   plan->bg = bg;
   plan->cvr = cvr;
   return MSDA_OK;
@@ -2411,6 +2605,23 @@ hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* bucke
     hipLaunchKernelGGL(msda_bucket_clear_kernel, dim3(blocks), dim3(256), lds, st, p, plan.bg, buckets);
   }
   const dim3 grid(unsigned(xcd_group_grid(p.H, int64_t(p.B) * plan.bucket_chunks))), block(kBucketThreads);
+  const size_t scan_lds = p.L > kMaxOrderedLevels ? (sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) : 0;
+  if (plan.bg.group4) {
+    auto run = [&](auto count, auto place) -> hipError_t {
+      hipError_t e = allow_lds(count, plan.bucket_lds);
+      if (e == hipSuccess) e = allow_lds(place, plan.bucket_lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(count, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
+                         int(plan.bucket_chunks));
+      hipLaunchKernelGGL(msda_bucket_scan_kernel, dim3(unsigned(p.B * p.H)), dim3(1024), scan_lds, st, p,
+                         plan.bg, buckets);
+      hipLaunchKernelGGL(place, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
+                         int(plan.bucket_chunks));
+      return hipGetLastError();
+    };
+    return plan.bg.key_bytes == 2 ? run(msda_bucket4_kernel<TL, false, 2>, msda_bucket4_kernel<TL, true, 2>)
+                                  : run(msda_bucket4_kernel<TL, false, 4>, msda_bucket4_kernel<TL, true, 4>);
+  }
   auto count = msda_bucket_kernel<TL, false>;
   auto place = msda_bucket_kernel<TL, true>;
   hipError_t e = allow_lds(count, plan.bucket_lds);
@@ -2418,7 +2629,6 @@ hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* bucke
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(count, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
                      int(plan.bucket_chunks));
-  const size_t scan_lds = p.L > kMaxOrderedLevels ? (sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) : 0;
   hipLaunchKernelGGL(msda_bucket_scan_kernel, dim3(unsigned(p.B * p.H)), dim3(1024), scan_lds, st, p,
                      plan.bg, buckets);
   hipLaunchKernelGGL(place, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
@@ -2608,10 +2818,10 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
     return fail(MSDA_ERR_INVALID, "msda_backward: null input tensor pointer");
   if (reinterpret_cast<uintptr_t>(grad_sampling_locations) % 4 != 0)
     return fail(MSDA_ERR_INVALID, "msda_backward: grad_sampling_locations must be 4-byte aligned");
-  const void* vec[] = {value, grad_output, grad_value};
+  const void* vec[] = {value, grad_output, grad_value, sampling_locations};
   BackwardPlan plan;
   rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
-                          loc_dtype, vec, 3, grad_attention_weights, device_lds_limit(), device_cus(),
+                          loc_dtype, vec, 4, grad_attention_weights, device_lds_limit(), device_cus(),
                           &plan);
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
