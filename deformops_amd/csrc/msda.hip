@@ -332,6 +332,13 @@ template <typename A> struct alignas(16) Staged {
   A w[4];
 };
 
+// The forward's staged sample for 16-bit values: the four corner offsets and the
+// weight pairs (w00, w01), (w10, w11) packed in the value dtype.
+struct alignas(8) StagedPk {
+  uint32_t off[4];
+  uint32_t w01, w23;
+};
+
 __device__ inline void load_levels(const Problem& p, Level* levels) {
   for (int i = threadIdx.x; i < p.L; i += blockDim.x) {
     int64_t h, w, st;
@@ -454,9 +461,8 @@ __device__ inline LaneMap map_lane(const Problem& p) {
 
 // Phase 1, shared by both directions: stage every sample of the lane's unit and
 // return the unit's softmax statistics (max and 1 / sum of exp), if any.
-// With PACK (16-bit value dtypes), w[0] and w[1] instead hold the bit patterns of
-// the weight pairs (w00, w01) and (w10, w11), each rounded to the value dtype, for
-// the forward's packed dot products.
+// With PACK (16-bit value dtypes), `wst` holds StagedPk records instead: the weight
+// pairs rounded to the value dtype, for the forward's packed dot products.
 template <typename T, typename TL, bool SOFTMAX, bool PACK = false>
 __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const Level* levels,
                                      Staged<typename Elem<T>::acc>* wst,
@@ -489,20 +495,23 @@ __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const L
                                   levels[s / p.P], head_bytes, pos_bytes);
     A a = load_acc(attn + s);
     if constexpr (SOFTMAX) a = exp_acc(a - smax) * sinv;
-    Staged<A> st;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) st.off[c] = g.off[c];
-    st.w[0] = g.w00 * a;
-    st.w[1] = g.w01 * a;
-    st.w[2] = g.w10 * a;
-    st.w[3] = g.w11 * a;
     if constexpr (PACK) {
-      const uint32_t w01 = Chan16<T, 2>::pack(st.w[0], st.w[1]);
-      const uint32_t w23 = Chan16<T, 2>::pack(st.w[2], st.w[3]);
-      st.w[0] = __uint_as_float(w01);
-      st.w[1] = __uint_as_float(w23);
+      StagedPk st;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) st.off[c] = g.off[c];
+      st.w01 = Chan16<T, 2>::pack(g.w00 * a, g.w01 * a);
+      st.w23 = Chan16<T, 2>::pack(g.w10 * a, g.w11 * a);
+      reinterpret_cast<StagedPk*>(wst)[s * m.uw_count + m.uw] = st;
+    } else {
+      Staged<A> st;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) st.off[c] = g.off[c];
+      st.w[0] = g.w00 * a;
+      st.w[1] = g.w01 * a;
+      st.w[2] = g.w10 * a;
+      st.w[3] = g.w11 * a;
+      wst[s * m.uw_count + m.uw] = st;
     }
-    wst[s * m.uw_count + m.uw] = st;
   }
 }
 
@@ -513,18 +522,17 @@ template <typename T, typename TL, int CV, bool SOFTMAX>
 __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel(const Problem p) {
   using A = typename Elem<T>::acc;
   constexpr int ES = Elem<T>::size;
-  extern __shared__ __align__(16) unsigned char smem[];
-  Level* levels = reinterpret_cast<Level*>(smem);
-  const LaneMap m = map_lane(p);
-  const int LP = p.L * p.P;
-  Staged<A>* wst = reinterpret_cast<Staged<A>*>(smem + sizeof(Level) * p.L) +
-                   m.wave * m.uw_count * LP;
-
   // 16-bit values: two corners per packed dot product. v_perm_b32 pairs channel i
   // of corners (0, 1), and of (2, 3); v_dot2_f32_{bf16,f16} multiplies the pair by
   // the staged weight pair (rounded to the value dtype) and adds to the fp32 sum:
   // one instruction per two products, no widening.
   constexpr bool kPacked = ES == 2 && CV >= 2;
+  extern __shared__ __align__(16) unsigned char smem[];
+  Level* levels = reinterpret_cast<Level*>(smem);
+  const LaneMap m = map_lane(p);
+  const int LP = p.L * p.P;
+  constexpr size_t kRec = kPacked ? sizeof(StagedPk) : sizeof(Staged<A>);
+  Staged<A>* wst = reinterpret_cast<Staged<A>*>(smem + sizeof(Level) * p.L + kRec * m.wave * m.uw_count * LP);
   load_levels(p, levels);
   __syncthreads();
   A smax, sinv;
@@ -539,13 +547,14 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
   for (int i = 0; i < CV; ++i) acc[i] = A(0);
   if constexpr (kPacked) {
     using R = typename Chan<T, CV>::R;
+    const StagedPk* wpk = reinterpret_cast<const StagedPk*>(wst);
 #pragma unroll 2
     for (int s = 0; s < LP; ++s) {
-      const Staged<A> st = wst[s * m.uw_count + m.uw];
+      const StagedPk st = wpk[s * m.uw_count + m.uw];
       R v[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c) v[c] = *reinterpret_cast<const R*>(img + (st.off[c] + lane_bytes));
-      const uint32_t w01 = __float_as_uint(st.w[0]), w23 = __float_as_uint(st.w[1]);
+      const uint32_t w01 = st.w01, w23 = st.w23;
 #pragma unroll
       for (int i = 0; i < CV / 2; ++i) {
         acc[2 * i] = dot2_16<T>(__builtin_amdgcn_perm(v[1].w[i], v[0].w[i], 0x05040100u), w01, acc[2 * i]);
@@ -2328,7 +2337,10 @@ int make_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, 
   int lh_log2 = 0;
   while ((1 << lh_log2) < lanes) ++lh_log2;
   const int uw = kWave >> lh_log2;
-  const size_t staged = (dtype == MSDA_F64) ? sizeof(Staged<double>) : sizeof(Staged<float>);
+  // The forward stages 16-bit weight pairs (StagedPk); the backward stages fp32 / fp64.
+  const size_t staged = (dtype == MSDA_F64)             ? sizeof(Staged<double>)
+                        : (!backward && es == 2 && cv >= 2) ? sizeof(StagedPk)
+                                                            : sizeof(Staged<float>);
   const size_t per_wave = size_t(uw) * size_t(L * P) * staged;
   const size_t levels_bytes = sizeof(Level) * size_t(L);
   if (levels_bytes + per_wave > kMaxLds)
@@ -2344,7 +2356,6 @@ int make_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, 
     if (levels_bytes + per_wave * waves <= kMaxLds && blocks >= 2048) break;
     waves >>= 1;
   }
-  (void)backward;
   plan->cv = cv;
   plan->lh_log2 = lh_log2;
   plan->waves = waves;
