@@ -1819,6 +1819,79 @@ __device__ inline void mfma_kblock(const MfmaTile& t, const Level& lv, uint32_t 
   }
 }
 
+// The K-blocks kb0, kb0 + kbstep, ... of one tile into acc (zeroed here). Two
+// register sets in turn: block j's entries are loaded two blocks ahead and its data
+// one block ahead, each before the loads of the block after, so that a wait for
+// one never waits for younger loads; while block j computes, the data of j + 1 and
+// the entries of j + 2 are in flight. The main loop issues its loads
+// unconditionally (an entry past the end reads candidate 0), so that the compiler's
+// wait counts stay exact; the last one or two blocks run after it.
+template <typename T, typename TL, int NB, bool SOFTMAX>
+__device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, const CandRanges& cr,
+                                         const uint32_t* __restrict__ ent, int kb0, int kbstep, int lane,
+                                         unsigned char* gst, unsigned char* wt, f32x4_v (&acc)[4][NB]) {
+#pragma unroll
+  for (int st = 0; st < 4; ++st)
+#pragma unroll
+    for (int j = 0; j < NB; ++j) acc[st][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+  const uint32_t nkb = (cr.ncand + kMfmaK - 1) / kMfmaK;
+  const uint32_t mine = nkb > uint32_t(kb0) ? (nkb - uint32_t(kb0) + uint32_t(kbstep) - 1) / uint32_t(kbstep) : 0u;
+  const uint32_t step = uint32_t(kbstep) * kMfmaK;
+  uint32_t cand = uint32_t(kb0) * kMfmaK + uint32_t(lane);  // this lane's candidate in block j
+  MfmaBlock<T, TL, NB> ba, bb;
+  uint32_t ea = 0, eb = 0, j = 0;
+  if (mine > 0) {
+    ea = cand_entry(ent, cr, cand);
+    eb = cand_entry(ent, cr, cand + step);
+    mfma_load<T, TL, NB, SOFTMAX>(t, ea, lane, ba);
+  }
+  for (; j + 2 < mine; j += 2) {
+    const uint32_t kb = uint32_t(kb0) + j * uint32_t(kbstep);
+    const uint32_t e2 = cand_entry(ent, cr, cand + 2 * step);
+    mfma_load<T, TL, NB, SOFTMAX>(t, eb, lane, bb);
+    mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ba, lane, gst, wt, acc);
+    const uint32_t e3 = cand_entry(ent, cr, cand + 3 * step);
+    mfma_load<T, TL, NB, SOFTMAX>(t, e2, lane, ba);
+    mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, bb, lane, gst, wt, acc);
+    ea = e2;
+    eb = e3;
+    cand += 2 * step;
+  }
+  if (j < mine) {
+    const uint32_t kb = uint32_t(kb0) + j * uint32_t(kbstep);
+    if (j + 1 < mine) mfma_load<T, TL, NB, SOFTMAX>(t, eb, lane, bb);
+    mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ba, lane, gst, wt, acc);
+    if (j + 1 < mine) mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, bb, lane, gst, wt, acc);
+  }
+}
+
+// Writes sub-tile st of a tile from the MFMA layout: lane l holds C[4 g + r][16 nb + i]
+// = position (r0 + 4 (st / 2) + g, c0 + 4 (st % 2) + r), channel 16 nb + i. The tile
+// owns these grad_value elements: one plain store each (a load-add-store with
+// `accumulate`).
+template <typename T, int NB>
+__device__ inline void mfma_store_subtile(const Problem& p, const Level& lv, const MfmaTile& t, int b, int h,
+                                          int st, const f32x4_v (&c)[NB], int g16, int i16, int accumulate,
+                                          T* gv) {
+  constexpr int D = 16 * NB;
+  const int y = t.r0 + 4 * (st >> 1) + g16;
+  if (y >= t.r1) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int x = t.c0 + 4 * (st & 1) + r;
+    if (x < t.c1) {
+      const int64_t pos = int64_t(b) * p.S + lv.start + int64_t(y) * lv.w + x;
+      T* dst = gv + (pos * p.H + h) * D + i16;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        float v = c[nb][r];
+        if (accumulate) v += load_acc(dst + 16 * nb);
+        store_elem(dst + 16 * nb, v);
+      }
+    }
+  }
+}
+
 // Workgroups per CU the register budget of the matrix-core kernel allows.
 constexpr int mfma_blocks_per_cu(int nb) { return nb == 1 ? 4 : nb == 2 ? 3 : 2; }
 
@@ -1972,183 +2045,141 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
   __syncthreads();
   const int g16 = lane >> 4, i16 = lane & 15;
 
-  // Thread 0: the rest of the current chunk, tasks [cur_local, cur_end) of entry cur_i.
-  int cur_i = 0, cur_local = 0, cur_end = 0;
+  // Thread 0 takes chunks from the queue and publishes them in chunk_s: entry i
+  // (-1: the queue is empty) and its tasks [first, last). Regional chunks of light
+  // levels (chunk size >= 4) run one task per wave with no partial sums to merge;
+  // the others run one task at a time, its K-blocks split over the four waves.
+  __shared__ int chunk_s[3];
   for (;;) {
     if (tid == 0) {
-      // -1: the queue is empty. Regional: entry i and task `local` in it; a chunk's
-      // tasks are queue neighbours and share their queries' cache lines.
-      int64_t got = -1;
+      int ci = -1, first = 0, last = 0;
+      const int64_t c = atomicAdd(queue, 1);
+      if (c < queue_len) {
+        if (regional) {
+          int lo = 0, hi = int(nentries) - 1;  // the last entry whose prefix is <= c
+          while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (table[mid] <= c) lo = mid; else hi = mid - 1;
+          }
+          const int cs = csz[lo % p.L];
+          ci = lo;
+          first = int(c - table[lo]) * cs;
+          last = min(first + cs, ntab[lo]);
+        } else {
+          ci = 0;
+          first = int(c);
+          last = first + 1;
+        }
+      }
+      chunk_s[0] = ci;
+      chunk_s[1] = first;
+      chunk_s[2] = last;
+    }
+    __syncthreads();
+    const int ci = chunk_s[0], first = chunk_s[1], last = chunk_s[2];
+    if (ci < 0) break;  // uniform: every thread read the same value
+    const bool per_wave = regional && csz[ci % p.L] >= kMfmaWaves;
+    const int step = per_wave ? kMfmaWaves : 1;
+    for (int base = first; base < last; base += step) {
+      const int local = per_wave ? base + wave : base;
+      if (local >= last) continue;  // only in the per-wave mode, where waves do not sync
+      // The task: level l, image b, head h, tile.
+      int l, b, h, tile;
       if (regional) {
-        if (cur_local >= cur_end) {
-          const int64_t c = atomicAdd(queue, 1);
-          cur_i = -1;
-          if (c < queue_len) {
-            int lo = 0, hi = int(nentries) - 1;  // the last entry whose prefix is <= c
-            while (lo < hi) {
-              const int mid = (lo + hi + 1) >> 1;
-              if (table[mid] <= c) lo = mid; else hi = mid - 1;
-            }
-            const int cs = csz[lo % p.L];
-            cur_i = lo;
-            cur_local = int(c - table[lo]) * cs;
-            cur_end = min(cur_local + cs, ntab[lo]);
-          }
-        }
-        if (cur_i >= 0) got = (int64_t(cur_i) << 32) | cur_local++;
+        const int64_t pair = pa + ci / p.L;
+        l = order[ci % p.L];
+        b = int(pair / (R * R));
+        int rx, ry;
+        morton_decode(int(pair % (R * R)), &rx, &ry);
+        const Level lvr = levels[l];
+        const LevelTiles tlr = lt[l];
+        const int tx0 = region_first_tile(rx, R, lvr.w, tlr.ntx);
+        const int nx = region_first_tile(rx + 1, R, lvr.w, tlr.ntx) - tx0;
+        const int ty0 = region_first_tile(ry, R, lvr.h, tlr.nty);
+        h = local % p.H;
+        const int rest = local / p.H;
+        tile = (ty0 + rest / nx) * tlr.ntx + tx0 + rest % nx;
       } else {
-        const int64_t k = atomicAdd(queue, 1);
-        got = k < queue_len ? k : -1;
-      }
-      total[1] = got;
-    }
-    __syncthreads();
-    const int64_t got = total[1];
-    if (got < 0) break;  // uniform: every thread read the same value
-    int l, b, h, tile;
-    if (regional) {
-      const int i = int(got >> 32), local = int(got & 0xffffffff);
-      const int64_t pair = pa + i / p.L;
-      l = order[i % p.L];
-      b = int(pair / (R * R));
-      int rx, ry;
-      morton_decode(int(pair % (R * R)), &rx, &ry);
-      const Level lvr = levels[l];
-      const LevelTiles tlr = lt[l];
-      const int tx0 = region_first_tile(rx, R, lvr.w, tlr.ntx);
-      const int nx = region_first_tile(rx + 1, R, lvr.w, tlr.ntx) - tx0;
-      const int ty0 = region_first_tile(ry, R, lvr.h, tlr.nty);
-      h = local % p.H;
-      const int rest = local / p.H;
-      tile = (ty0 + rest / nx) * tlr.ntx + tx0 + rest % nx;
-    } else {
-      int64_t k = got;
-      // The queue's k-th task: level order[oi], task t of that level.
-      int oi = 0;
-      int64_t tl_task = 0;
-      for (; oi < p.L; ++oi) {
-        const int64_t n = int64_t(rank_base[oi + 1] - rank_base[oi]) * per_tile;
-        const int64_t lo = xcd * n / kXcds, len = (xcd + 1) * n / kXcds - lo;
-        if (k < len) {
-          tl_task = lo + k;
-          break;
-        }
-        k -= len;
-      }
-      l = order[oi];
-      const LevelTiles tlr = lt[l];
-      const int ntl = tlr.ntx * tlr.nty;
-      h = int(tl_task % p.H);
-      const int64_t rest = tl_task / p.H;
-      tile = int(rest % ntl);
-      b = int(rest / ntl);
-    }
-    const Level lv = levels[l];
-    const LevelTiles tl = lt[l];
-    const int ty = tile / tl.ntx, tx = tile - ty * tl.ntx;
-    const int bh = b * p.H + h;
-    const uint32_t* ent = entries + int64_t(bh) * bg.region;
-    const CandRanges cr = tile_candidates(buckets + int64_t(bh) * 4 * ntiles, tl, tile, tx, ty, uint32_t(l * p.P));
-    const int64_t unit0 = int64_t(b) * p.Q * p.H + h;  // (b, q = 0, h)
-    MfmaTile t;
-    t.loc = p.loc + unit0 * LP * 2 * int64_t(sizeof(TL));
-    t.attn = p.attn + unit0 * LP * ES;
-    t.gout = p.grad_out + unit0 * D * ES;
-    t.loc_q = uint32_t(p.H * LP * 2) * uint32_t(sizeof(TL));
-    t.attn_q = uint32_t(p.H * LP * ES);
-    t.gout_q = uint32_t(p.H * D * ES);
-    t.r0 = ty << kMfmaSubLog2;
-    t.c0 = tx << kMfmaSubLog2;
-    t.r1 = min(t.r0 + (1 << kMfmaSubLog2), lv.h);
-    t.c1 = min(t.c0 + (1 << kMfmaSubLog2), lv.w);
-    t.ncand = cr.ncand;
-    t.div_lp = bg.div_lp;
-    t.LP = LP;
-
-    f32x4_v acc[4][NB];
-#pragma unroll
-    for (int st = 0; st < 4; ++st)
-#pragma unroll
-      for (int j = 0; j < NB; ++j) acc[st][j] = f32x4_v{0.f, 0.f, 0.f, 0.f};
-
-    // This wave's K-blocks: wave, wave + 4, ...; two register sets in turn. Block
-    // j's entries are loaded two blocks ahead and its data one block ahead, each
-    // before the loads of the block after, so that a wait for one never waits for
-    // younger loads: while block j computes, the data of j + 1 and the entries of
-    // j + 2 are in flight.
-    const uint32_t nkb = (cr.ncand + kMfmaK - 1) / kMfmaK;
-    const uint32_t mine = nkb > uint32_t(wave) ? (nkb - uint32_t(wave) + kMfmaWaves - 1) / kMfmaWaves : 0u;
-    const uint32_t step = kMfmaWaves * kMfmaK;
-    uint32_t cand = uint32_t(wave) * kMfmaK + uint32_t(lane);  // this lane's candidate in block j
-    // The main loop issues its loads unconditionally (an entry past the end reads
-    // candidate 0), so that the compiler's wait counts stay exact; the last one or
-    // two blocks run after it.
-    MfmaBlock<T, TL, NB> ba, bb;
-    uint32_t ea = 0, eb = 0, j = 0;
-    if (mine > 0) {
-      ea = cand_entry(ent, cr, cand);
-      eb = cand_entry(ent, cr, cand + step);
-      mfma_load<T, TL, NB, SOFTMAX>(t, ea, lane, ba);
-    }
-    for (; j + 2 < mine; j += 2) {
-      const uint32_t kb = uint32_t(wave) + j * kMfmaWaves;
-      const uint32_t e2 = cand_entry(ent, cr, cand + 2 * step);
-      mfma_load<T, TL, NB, SOFTMAX>(t, eb, lane, bb);
-      mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ba, lane, gst, wt, acc);
-      const uint32_t e3 = cand_entry(ent, cr, cand + 3 * step);
-      mfma_load<T, TL, NB, SOFTMAX>(t, e2, lane, ba);
-      mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb + kMfmaWaves, eb, bb, lane, gst, wt, acc);
-      ea = e2;
-      eb = e3;
-      cand += 2 * step;
-    }
-    if (j < mine) {
-      const uint32_t kb = uint32_t(wave) + j * kMfmaWaves;
-      if (j + 1 < mine) mfma_load<T, TL, NB, SOFTMAX>(t, eb, lane, bb);
-      mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ba, lane, gst, wt, acc);
-      if (j + 1 < mine) mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb + kMfmaWaves, eb, bb, lane, gst, wt, acc);
-    }
-
-    // Partial sums meet in LDS (each wave's own region, which only it used so far):
-    // wave w adds the four waves' sums of sub-tile w.
-    {
-      u32x4_v* out = reinterpret_cast<u32x4_v*>(gst);
-#pragma unroll
-      for (int st = 0; st < 4; ++st)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) out[(st * NB + nb) * kWave + lane] = __builtin_bit_cast(u32x4_v, acc[st][nb]);
-    }
-    __syncthreads();
-    f32x4_v sum[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      sum[nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int w = 0; w < kMfmaWaves; ++w)
-        sum[nb] += __builtin_bit_cast(
-            f32x4_v, reinterpret_cast<const u32x4_v*>(region0 + size_t(w) * kWaveBytes)[(wave * NB + nb) * kWave + lane]);
-    }
-    // Lane l holds C[4 g + r][16 nb + i] of sub-tile `wave`: position
-    // (r0 + 4 (wave / 2) + g, c0 + 4 (wave % 2) + r), channel 16 nb + i.
-    const int y = t.r0 + 4 * (wave >> 1) + g16;
-    if (y < t.r1) {
-      T* gv = reinterpret_cast<T*>(p.grad_value);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int x = t.c0 + 4 * (wave & 1) + r;
-        if (x < t.c1) {
-          const int64_t pos = int64_t(b) * p.S + lv.start + int64_t(y) * lv.w + x;
-          T* dst = gv + (pos * p.H + h) * D + i16;
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            float v = sum[nb][r];
-            if (accumulate) v += load_acc(dst + 16 * nb);
-            store_elem(dst + 16 * nb, v);
+        int64_t k = local;
+        // The queue's k-th task: level order[oi], task t of that level.
+        int oi = 0;
+        int64_t tl_task = 0;
+        for (; oi < p.L; ++oi) {
+          const int64_t n = int64_t(rank_base[oi + 1] - rank_base[oi]) * per_tile;
+          const int64_t lo = xcd * n / kXcds, len = (xcd + 1) * n / kXcds - lo;
+          if (k < len) {
+            tl_task = lo + k;
+            break;
           }
+          k -= len;
         }
+        l = order[oi];
+        const LevelTiles tlr = lt[l];
+        const int ntl = tlr.ntx * tlr.nty;
+        h = int(tl_task % p.H);
+        const int64_t rest = tl_task / p.H;
+        tile = int(rest % ntl);
+        b = int(rest / ntl);
       }
+      const Level lv = levels[l];
+      const LevelTiles tl = lt[l];
+      const int ty = tile / tl.ntx, tx = tile - ty * tl.ntx;
+      const int bh = b * p.H + h;
+      const uint32_t* ent = entries + int64_t(bh) * bg.region;
+      const CandRanges cr = tile_candidates(buckets + int64_t(bh) * 4 * ntiles, tl, tile, tx, ty, uint32_t(l * p.P));
+      const int64_t unit0 = int64_t(b) * p.Q * p.H + h;  // (b, q = 0, h)
+      MfmaTile t;
+      t.loc = p.loc + unit0 * LP * 2 * int64_t(sizeof(TL));
+      t.attn = p.attn + unit0 * LP * ES;
+      t.gout = p.grad_out + unit0 * D * ES;
+      t.loc_q = uint32_t(p.H * LP * 2) * uint32_t(sizeof(TL));
+      t.attn_q = uint32_t(p.H * LP * ES);
+      t.gout_q = uint32_t(p.H * D * ES);
+      t.r0 = ty << kMfmaSubLog2;
+      t.c0 = tx << kMfmaSubLog2;
+      t.r1 = min(t.r0 + (1 << kMfmaSubLog2), lv.h);
+      t.c1 = min(t.c0 + (1 << kMfmaSubLog2), lv.w);
+      t.ncand = cr.ncand;
+      t.div_lp = bg.div_lp;
+      t.LP = LP;
+
+      f32x4_v acc[4][NB];
+      // All K-blocks (per-wave mode), or K-blocks wave, wave + 4, ...
+      mfma_tile_kblocks<T, TL, NB, SOFTMAX>(t, lv, cr, ent, per_wave ? 0 : wave, per_wave ? 1 : kMfmaWaves,
+                                            lane, gst, wt, acc);
+
+      T* gv = reinterpret_cast<T*>(p.grad_value);
+      if (per_wave) {
+        // Lane l holds C[4 g + r][16 nb + i] of sub-tile st: position
+        // (r0 + 4 (st / 2) + g, c0 + 4 (st % 2) + r), channel 16 nb + i.
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+          mfma_store_subtile<T, NB>(p, lv, t, b, h, st, acc[st], g16, i16, accumulate, gv);
+        continue;
+      }
+      // Partial sums meet in LDS (each wave's own region, which only it used so
+      // far): wave w adds the four waves' sums of sub-tile w.
+      {
+        u32x4_v* out = reinterpret_cast<u32x4_v*>(gst);
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) out[(st * NB + nb) * kWave + lane] = __builtin_bit_cast(u32x4_v, acc[st][nb]);
+      }
+      __syncthreads();
+      f32x4_v sum[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        sum[nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < kMfmaWaves; ++w)
+          sum[nb] += __builtin_bit_cast(
+              f32x4_v, reinterpret_cast<const u32x4_v*>(region0 + size_t(w) * kWaveBytes)[(wave * NB + nb) * kWave + lane]);
+      }
+      mfma_store_subtile<T, NB>(p, lv, t, b, h, wave, sum, g16, i16, accumulate, gv);
+      __syncthreads();  // the partial sums are read before the next tile reuses the LDS
     }
-    __syncthreads();  // the partial sums are read before the next tile reuses the LDS
+    __syncthreads();  // every wave is done with the chunk before the next one is published
   }
 }
 
