@@ -1624,6 +1624,10 @@ template <> struct MfmaOp<f16_t> {
   static __device__ inline uint16_t round(float w) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(w)); }
 };
 
+// A wave-uniform value moved to a scalar register (it is the same in every lane).
+__device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ inline uint32_t uni(uint32_t v) { return uint32_t(__builtin_amdgcn_readfirstlane(int(v))); }
+
 // Keeps the compiler from moving this wave's LDS accesses across it. The LDS
 // executes one wave's instructions in order, so lanes of a wave then see each
 // other's earlier writes without a barrier.
@@ -1681,14 +1685,14 @@ __device__ inline CandRanges tile_candidates(const int* __restrict__ brow, const
     }
   }
   CandRanges r;
-  r.n0 = rn[0];
-  r.n01 = rn[0] + rn[1];
-  r.n012 = r.n01 + rn[2];
-  r.ncand = r.n012 + rn[3];
-  r.off0 = rs[0];
-  r.off1 = rs[1] - r.n0;
-  r.off2 = rs[2] - r.n01;
-  r.off3 = rs[3] - r.n012;
+  r.n0 = uni(rn[0]);
+  r.n01 = uni(rn[0] + rn[1]);
+  r.n012 = uni(r.n01 + rn[2]);
+  r.ncand = uni(r.n012 + rn[3]);
+  r.off0 = uni(rs[0]);
+  r.off1 = uni(rs[1] - r.n0);
+  r.off2 = uni(rs[2] - r.n01);
+  r.off3 = uni(rs[3] - r.n012);
   r.stand_in = stand_in;
   return r;
 }
@@ -1703,11 +1707,15 @@ __device__ inline uint32_t cand_entry(const uint32_t* __restrict__ ent, const Ca
   return ent[c + off];
 }
 
-// One K-block's loads for one lane: its candidate's location and weight, and its
-// share of the block's grad_out rows (flat 16-byte piece lane + 64 j of 64 rows).
-template <typename T, typename TL, int NB> struct MfmaBlock {
+// One K-block's loads for one lane: its candidate's location and weight (MfmaMeta,
+// loaded a block ahead), and its share of the block's grad_out rows (MfmaRows: flat
+// 16-byte piece lane + 64 j of the 64 rows, loaded half a block ahead, as soon as
+// the previous block has staged its rows).
+template <typename T, typename TL> struct MfmaMeta {
   LocPair<TL> loc;
   T attn;
+};
+template <int NB> struct MfmaRows {
   u32x4_v piece[2 * NB];
 };
 
@@ -1723,44 +1731,54 @@ struct MfmaTile {
   int LP;
 };
 
-template <typename T, typename TL, int NB, bool SOFTMAX>
-__device__ inline void mfma_load(const MfmaTile& t, uint32_t e, int lane, MfmaBlock<T, TL, NB>& d) {
-  constexpr int kPieces = NB * 2;  // 16-byte pieces per grad_out row (2 * 16 NB bytes)
+template <typename T, typename TL, bool SOFTMAX>
+__device__ inline void mfma_load_meta(const MfmaTile& t, uint32_t e, MfmaMeta<T, TL>& d) {
   const uint32_t q = fdiv(e, t.div_lp), s = e - q * uint32_t(t.LP);
-  d.loc = *reinterpret_cast<const LocPair<TL>*>(t.loc + (q * t.loc_q + s * uint32_t(2 * sizeof(TL))));
-  if constexpr (!SOFTMAX) d.attn = *reinterpret_cast<const T*>(t.attn + (q * t.attn_q + s * 2u));
+  d.loc = *reinterpret_cast<const LocPair<TL>*>(t.loc + (__umul24(q, t.loc_q) + s * uint32_t(2 * sizeof(TL))));
+  if constexpr (!SOFTMAX) d.attn = *reinterpret_cast<const T*>(t.attn + (__umul24(q, t.attn_q) + s * 2u));
+}
+
+template <int NB>
+__device__ inline void mfma_load_rows(const MfmaTile& t, uint32_t e, int lane, MfmaRows<NB>& d) {
+  constexpr int kPieces = NB * 2;  // 16-byte pieces per grad_out row (2 * 16 NB bytes)
+  const uint32_t q = fdiv(e, t.div_lp);
 #pragma unroll
   for (int j = 0; j < 2 * NB; ++j) {
     const int f = lane + kWave * j, row = f / kPieces, pc = f - row * kPieces;
     const uint32_t qr = uint32_t(__shfl(int(q), row));
-    d.piece[j] = *reinterpret_cast<const u32x4_v*>(t.gout + (qr * t.gout_q + uint32_t(pc * 16)));
+    d.piece[j] = *reinterpret_cast<const u32x4_v*>(t.gout + (__umul24(qr, t.gout_q) + uint32_t(pc * 16)));
   }
 }
 
-// One K-block of one wave: stage the 64 grad_out rows, then per MFMA K-step (the
-// candidates of lanes 0-31, then 32-63) scatter their corner weights into the four
-// zeroed weight tiles and run the four sub-tiles' MFMAs.
+// One K-block of one wave, in two parts. Part A: the candidate's corners (as LDS
+// byte offsets of their weights in the four weight tiles, -1 outside the tile, and
+// the weights rounded to the value dtype), and the block's 64 grad_out rows into
+// LDS, after which the row registers are free for the next block's loads. Part B:
+// per MFMA K-step (the candidates of lanes 0-31, then 32-63) scatter the corner
+// weights into the zeroed weight tiles and run the four sub-tiles' MFMAs.
+struct MfmaCorners {
+  int o[4];
+  uint16_t w[4];
+};
+
 template <typename T, typename TL, int NB, bool SOFTMAX>
-__device__ inline void mfma_kblock(const MfmaTile& t, const Level& lv, uint32_t kb, uint32_t e,
-                                   const MfmaBlock<T, TL, NB>& d, int lane, unsigned char* gst,
-                                   unsigned char* wt, f32x4_v (&acc)[4][NB]) {
+__device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, uint32_t kb, uint32_t e,
+                                           const MfmaMeta<T, TL>& d, const MfmaRows<NB>& rows, int lane,
+                                           unsigned char* gst) {
   using Op = MfmaOp<T>;
-  using V = typename Op::V;
-  constexpr int kRowBytes = 32 * NB;
   constexpr int kPieces = NB * 2;
-  const int kc = lane & (kMfmaKStep - 1), half = lane >> 5;
-  const int g16 = lane >> 4, i16 = lane & 15;
+  const int kc = lane & (kMfmaKStep - 1);
   const uint32_t c = kb * kMfmaK + uint32_t(lane);
-  // The candidate's four corners as LDS byte offsets of their weights in the tiles
-  // (-1: not in the tile).
-  int o[4] = {-1, -1, -1, -1};
+  MfmaCorners cr;
   float w[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) cr.o[k] = -1;
   if (c < t.ncand) {
     const Geom<float> g = geometry<float>(to_acc(d.loc.x), to_acc(d.loc.y), lv, 0u, 1u);
     float a;
     if constexpr (SOFTMAX) {
       const uint32_t q = fdiv(e, t.div_lp), s = e - q * uint32_t(t.LP);
-      a = unit_weight<T, true>(reinterpret_cast<const T*>(t.attn + q * t.attn_q), t.LP, int(s));
+      a = unit_weight<T, true>(reinterpret_cast<const T*>(t.attn + __umul24(q, t.attn_q)), t.LP, int(s));
     } else {
       a = to_acc(d.attn);
     }
@@ -1772,22 +1790,33 @@ __device__ inline void mfma_kblock(const MfmaTile& t, const Level& lv, uint32_t 
       const int y = y0 + (k >> 1), x = x0 + (k & 1);
       // Position (y, x) of the tile: sub-tile (y / 4) * 2 + x / 4, row (y % 4) * 4 + x % 4.
       if (m[k] && y >= 0 && x >= 0 && t.r0 + y < t.r1 && t.c0 + x < t.c1) {
-        o[k] = ((y >> 2) * 2 + (x >> 2)) * kMfmaWBytes + ((y & 3) * 4 + (x & 3)) * (2 * kMfmaKStep) + kc * 2;
+        cr.o[k] = ((y >> 2) * 2 + (x >> 2)) * kMfmaWBytes + ((y & 3) * 4 + (x & 3)) * (2 * kMfmaKStep) + kc * 2;
         w[k] = wb[k] * a;
       }
     }
   }
-  uint16_t wr[4];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) wr[k] = Op::round(w[k]);
+  for (int k = 0; k < 4; ++k) cr.w[k] = Op::round(w[k]);
   wave_lds_order();  // after the previous K-block's operand reads
   const u32x4_v zero = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int j = 0; j < 2 * NB; ++j) {
     const int f = lane + kWave * j, row = f / kPieces;
     const bool ok = kb * kMfmaK + uint32_t(row) < t.ncand;  // past the end: zero rows
-    *reinterpret_cast<u32x4_v*>(gst + f * 16) = ok ? d.piece[j] : zero;
+    *reinterpret_cast<u32x4_v*>(gst + f * 16) = ok ? rows.piece[j] : zero;
   }
+  return cr;
+}
+
+template <typename T, int NB>
+__device__ inline void mfma_kblock_b(const MfmaCorners& cr, int lane, const unsigned char* gst,
+                                     unsigned char* wt, f32x4_v (&acc)[4][NB]) {
+  using Op = MfmaOp<T>;
+  using V = typename Op::V;
+  constexpr int kRowBytes = 32 * NB;
+  const int half = lane >> 5;
+  const int g16 = lane >> 4, i16 = lane & 15;
+  const u32x4_v zero = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     wave_lds_order();
@@ -1797,7 +1826,7 @@ __device__ inline void mfma_kblock(const MfmaTile& t, const Level& lv, uint32_t 
     if (half == ks) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        if (o[k] >= 0) *reinterpret_cast<uint16_t*>(wt + o[k]) = wr[k];
+        if (cr.o[k] >= 0) *reinterpret_cast<uint16_t*>(wt + cr.o[k]) = cr.w[k];
     }
     wave_lds_order();
     V bv[NB];
@@ -1819,13 +1848,13 @@ __device__ inline void mfma_kblock(const MfmaTile& t, const Level& lv, uint32_t 
   }
 }
 
-// The K-blocks kb0, kb0 + kbstep, ... of one tile into acc (zeroed here). Two
-// register sets in turn: block j's entries are loaded two blocks ahead and its data
-// one block ahead, each before the loads of the block after, so that a wait for
-// one never waits for younger loads; while block j computes, the data of j + 1 and
-// the entries of j + 2 are in flight. The main loop issues its loads
-// unconditionally (an entry past the end reads candidate 0), so that the compiler's
-// wait counts stay exact; the last one or two blocks run after it.
+// The K-blocks kb0, kb0 + kbstep, ... of one tile into acc (zeroed here). Block j's
+// entries are loaded two blocks ahead, its locations and weights one block ahead
+// (two register sets in turn) and its grad_out rows as soon as block j - 1 has
+// staged its own, each before the loads of later blocks, so that a wait for one
+// never waits for younger loads. The main loop issues its loads unconditionally
+// (an entry past the end reads candidate 0), so that the compiler's wait counts
+// stay exact; the last one or two blocks run after it.
 template <typename T, typename TL, int NB, bool SOFTMAX>
 __device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, const CandRanges& cr,
                                          const uint32_t* __restrict__ ent, int kb0, int kbstep, int lane,
@@ -1838,30 +1867,42 @@ __device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, con
   const uint32_t mine = nkb > uint32_t(kb0) ? (nkb - uint32_t(kb0) + uint32_t(kbstep) - 1) / uint32_t(kbstep) : 0u;
   const uint32_t step = uint32_t(kbstep) * kMfmaK;
   uint32_t cand = uint32_t(kb0) * kMfmaK + uint32_t(lane);  // this lane's candidate in block j
-  MfmaBlock<T, TL, NB> ba, bb;
+  MfmaMeta<T, TL> ma, mb;
+  MfmaRows<NB> rows;
   uint32_t ea = 0, eb = 0, j = 0;
   if (mine > 0) {
     ea = cand_entry(ent, cr, cand);
     eb = cand_entry(ent, cr, cand + step);
-    mfma_load<T, TL, NB, SOFTMAX>(t, ea, lane, ba);
+    mfma_load_meta<T, TL, SOFTMAX>(t, ea, ma);
+    mfma_load_rows<NB>(t, ea, lane, rows);
   }
   for (; j + 2 < mine; j += 2) {
     const uint32_t kb = uint32_t(kb0) + j * uint32_t(kbstep);
     const uint32_t e2 = cand_entry(ent, cr, cand + 2 * step);
-    mfma_load<T, TL, NB, SOFTMAX>(t, eb, lane, bb);
-    mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ba, lane, gst, wt, acc);
+    mfma_load_meta<T, TL, SOFTMAX>(t, eb, mb);
+    MfmaCorners c0 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ma, rows, lane, gst);
+    mfma_load_rows<NB>(t, eb, lane, rows);
+    mfma_kblock_b<T, NB>(c0, lane, gst, wt, acc);
     const uint32_t e3 = cand_entry(ent, cr, cand + 3 * step);
-    mfma_load<T, TL, NB, SOFTMAX>(t, e2, lane, ba);
-    mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, bb, lane, gst, wt, acc);
+    mfma_load_meta<T, TL, SOFTMAX>(t, e2, ma);
+    MfmaCorners c1 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, mb, rows, lane, gst);
+    mfma_load_rows<NB>(t, e2, lane, rows);
+    mfma_kblock_b<T, NB>(c1, lane, gst, wt, acc);
     ea = e2;
     eb = e3;
     cand += 2 * step;
   }
   if (j < mine) {
     const uint32_t kb = uint32_t(kb0) + j * uint32_t(kbstep);
-    if (j + 1 < mine) mfma_load<T, TL, NB, SOFTMAX>(t, eb, lane, bb);
-    mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ba, lane, gst, wt, acc);
-    if (j + 1 < mine) mfma_kblock<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, bb, lane, gst, wt, acc);
+    const bool two = j + 1 < mine;
+    if (two) mfma_load_meta<T, TL, SOFTMAX>(t, eb, mb);
+    MfmaCorners c0 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ma, rows, lane, gst);
+    if (two) mfma_load_rows<NB>(t, eb, lane, rows);
+    mfma_kblock_b<T, NB>(c0, lane, gst, wt, acc);
+    if (two) {
+      MfmaCorners c1 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, mb, rows, lane, gst);
+      mfma_kblock_b<T, NB>(c1, lane, gst, wt, acc);
+    }
   }
 }
 
@@ -2121,8 +2162,14 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
         tile = int(rest % ntl);
         b = int(rest / ntl);
       }
-      const Level lv = levels[l];
-      const LevelTiles tl = lt[l];
+      l = uni(l);
+      b = uni(b);
+      h = uni(h);
+      tile = uni(tile);
+      Level lv = levels[l];
+      lv = Level{uni(lv.h), uni(lv.w), uni(lv.start), uni(lv.ok)};
+      LevelTiles tl = lt[l];
+      tl = LevelTiles{uni(tl.lh), uni(tl.lw), uni(tl.ntx), uni(tl.nty), uni(tl.base)};
       const int ty = tile / tl.ntx, tx = tile - ty * tl.ntx;
       const int bh = b * p.H + h;
       const uint32_t* ent = entries + int64_t(bh) * bg.region;
