@@ -34,6 +34,11 @@ from tests.workloads import CONFIGS, algorithmic_bytes, make_workload  # noqa: E
 
 METRIC = "MSDA fwd+bwd ms/call + achieved HBM GB/s, 21.5k-query bf16 encoder, 1 GPU"
 PEAK_HBM_GBS = 8000.0
+# HBM bytes of one backward C-ABI call on the default workload (bf16 value, weights
+# and locations, linear method): rocprofv3 FETCH_SIZE x 2 + WRITE_SIZE x 1, summed
+# over the call's kernels, each counter scaled by what it reads for a 256 MiB copy.
+# profiles/msda_config4_bf16_hbm_traffic.md holds the passes and the calibration.
+BACKWARD_TRAFFIC_BYTES = 1_261_519_052
 DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 
 
@@ -176,7 +181,7 @@ def main() -> int:
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
             "bench.py measures one GPU: the MSDA op shards by batch or heads with no "
-            "exchange (see DESIGN.md), and this build runs on a single MI355X. "
+            "exchange, and this build runs on a single MI355X. "
             "Run it with --gpus 1.",
             file=sys.stderr,
         )
@@ -209,6 +214,7 @@ def main() -> int:
     bwd_gbs = bwd_bytes / (kernels["backward"] * 1e-3) / 1e9
     total_gbs = (fwd_bytes + bwd_bytes) / (ms_per_step * 1e-3) / 1e9
 
+    profiled = args.dtype == "bf16" and loc_dtype == torch.bfloat16 and not softmax
     line = {
         "metric": METRIC,
         "value": round(ms_per_step, 5),
@@ -244,7 +250,7 @@ def main() -> int:
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
             "frac": round(bwd_gbs / PEAK_HBM_GBS, 4),
-            "traffic": None,
+            "traffic": BACKWARD_TRAFFIC_BYTES if profiled else None,
             "algorithmic_bytes_per_launch": bwd_bytes,
         },
     }
