@@ -314,6 +314,7 @@ struct Problem {
   int units_per_block;  // waves per block * units per wave
   int blocks_per_batch;
   int num_blocks;
+  int loc_piece, attn_piece;  // bytes per lane access copying a wave's records to LDS
 };
 
 // One pyramid level as the kernels use it. A level whose table entry does not fit
@@ -459,20 +460,73 @@ __device__ inline LaneMap map_lane(const Problem& p) {
   return m;
 }
 
+// Copies bytes from global memory to LDS, `piece` bytes (16, 8, 4, 2 or 1, dividing
+// `bytes` and the alignment of both ends) per lane and step.
+__device__ inline void copy_pieces(unsigned char* dst, const char* src, int bytes, int piece, int lane) {
+  if (piece == 16) {
+    for (int i = lane * 16; i < bytes; i += kWave * 16)
+      *reinterpret_cast<u32x4_v*>(dst + i) = *reinterpret_cast<const u32x4_v*>(src + i);
+  } else if (piece == 8) {
+    for (int i = lane * 8; i < bytes; i += kWave * 8)
+      *reinterpret_cast<u32x2_v*>(dst + i) = *reinterpret_cast<const u32x2_v*>(src + i);
+  } else if (piece == 4) {
+    for (int i = lane * 4; i < bytes; i += kWave * 4)
+      *reinterpret_cast<uint32_t*>(dst + i) = *reinterpret_cast<const uint32_t*>(src + i);
+  } else if (piece == 2) {
+    for (int i = lane * 2; i < bytes; i += kWave * 2)
+      *reinterpret_cast<uint16_t*>(dst + i) = *reinterpret_cast<const uint16_t*>(src + i);
+  } else {
+    for (int i = lane; i < bytes; i += kWave) dst[i] = static_cast<unsigned char>(src[i]);
+  }
+}
+
+// Bytes of one wave's LDS copy of its units' locations and weights (each part a
+// multiple of 16).
+__device__ __host__ inline int unit_raw_bytes(int uw_count, int LP, int loc_es, int es) {
+  return ((uw_count * LP * 2 * loc_es + 15) & ~15) + ((uw_count * LP * es + 15) & ~15);
+}
+
+// A lane's unit's locations and weights in the wave's LDS copy.
+struct UnitRaw {
+  const unsigned char* loc;
+  const unsigned char* attn;
+};
+
+// The wave's units are consecutive (b, q, h), so their locations and their weights
+// are two contiguous ranges: the wave copies both to its part of `raw_base` (which
+// follows the staged records of every wave) with wide coalesced loads, instead of
+// one 2- to 8-byte load per sample and coordinate. The copy is complete for the
+// other lanes after the next workgroup barrier.
+template <typename T, typename TL>
+__device__ inline UnitRaw copy_unit_records(const Problem& p, const LaneMap& m, unsigned char* raw_base) {
+  constexpr int ES = Elem<T>::size;
+  const int LP = p.L * p.P;
+  const int loc_unit = LP * 2 * int(sizeof(TL)), attn_unit = LP * ES;
+  const int loc_wave = (m.uw_count * loc_unit + 15) & ~15;
+  unsigned char* lds_loc = raw_base + size_t(m.wave) * size_t(unit_raw_bytes(m.uw_count, LP, int(sizeof(TL)), ES));
+  unsigned char* lds_attn = lds_loc + loc_wave;
+  const int first = m.unit - m.uw;  // the wave's first unit in its batch image
+  const int n = max(0, min(m.uw_count, p.Q * p.H - first));
+  const int64_t g0 = int64_t(m.b) * p.Q * p.H + first;
+  copy_pieces(lds_loc, p.loc + g0 * loc_unit, n * loc_unit, p.loc_piece, m.lane);
+  copy_pieces(lds_attn, p.attn + g0 * attn_unit, n * attn_unit, p.attn_piece, m.lane);
+  return UnitRaw{lds_loc + m.uw * loc_unit, lds_attn + m.uw * attn_unit};
+}
+
 // Phase 1, shared by both directions: stage every sample of the lane's unit and
 // return the unit's softmax statistics (max and 1 / sum of exp), if any.
 // With PACK (16-bit value dtypes), `wst` holds StagedPk records instead: the weight
 // pairs rounded to the value dtype, for the forward's packed dot products.
 template <typename T, typename TL, bool SOFTMAX, bool PACK = false>
 __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const Level* levels,
-                                     Staged<typename Elem<T>::acc>* wst,
+                                     const UnitRaw& raw, Staged<typename Elem<T>::acc>* wst,
                                      typename Elem<T>::acc& smax,
                                      typename Elem<T>::acc& sinv) {
   using A = typename Elem<T>::acc;
   constexpr int ES = Elem<T>::size;
   const int LP = p.L * p.P;
-  const TL* loc = reinterpret_cast<const TL*>(p.loc) + m.gunit * LP * 2;
-  const T* attn = reinterpret_cast<const T*>(p.attn) + m.gunit * LP;
+  const TL* loc = reinterpret_cast<const TL*>(raw.loc);
+  const T* attn = reinterpret_cast<const T*>(raw.attn);
   smax = A(0);
   sinv = A(1);
   if constexpr (SOFTMAX) {
@@ -533,10 +587,12 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
   const int LP = p.L * p.P;
   constexpr size_t kRec = kPacked ? sizeof(StagedPk) : sizeof(Staged<A>);
   Staged<A>* wst = reinterpret_cast<Staged<A>*>(smem + sizeof(Level) * p.L + kRec * m.wave * m.uw_count * LP);
+  const size_t raw_at = (sizeof(Level) * p.L + kRec * (blockDim.x / kWave) * m.uw_count * LP + 15) & ~size_t(15);
+  const UnitRaw raw = copy_unit_records<T, TL>(p, m, smem + raw_at);
   load_levels(p, levels);
   __syncthreads();
   A smax, sinv;
-  stage_samples<T, TL, SOFTMAX, kPacked>(p, m, levels, wst, smax, sinv);
+  stage_samples<T, TL, SOFTMAX, kPacked>(p, m, levels, raw, wst, smax, sinv);
   __syncthreads();
 
   if (!m.unit_ok || m.t * CV >= p.D) return;
@@ -2230,6 +2286,64 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
   }
 }
 
+// Samples of a unit whose corner loads grad_sample issues together.
+constexpr int kSampleBatch = 2;
+
+// G_c = <grad_out, value at corner c> for the staged samples s .. s + N - 1 of the
+// lane's unit, summed over the unit's lanes; the lane that staged a sample keeps its
+// G_c in the sample's slot. The corner loads of all N samples go out before the
+// first dot product (the cross-lane sums keep the compiler from unrolling a loop
+// over samples).
+template <typename T, int CV, int N>
+__device__ inline void corner_dots(const LaneMap& m, Staged<typename Elem<T>::acc>* wst, int s, bool lane_ok,
+                                   const char* img, uint32_t lane_bytes, const typename Chan<T, CV>::R& g) {
+  using A = typename Elem<T>::acc;
+  using R = typename Chan<T, CV>::R;
+  Staged<A> st[N];
+#pragma unroll
+  for (int n = 0; n < N; ++n) st[n] = wst[(s + n) * m.uw_count + m.uw];
+  A G[N][4];
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) G[n][c] = A(0);
+  if (lane_ok) {
+    R v[N][4];
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) v[n][c] = *reinterpret_cast<const R*>(img + (st[n].off[c] + lane_bytes));
+#pragma unroll
+    for (int n = 0; n < N; ++n)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) G[n][c] = Chan<T, CV>::dot(g, v[n][c], G[n][c]);
+  }
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) G[n][c] = unit_sum(G[n][c], m.lh);
+#pragma unroll
+  for (int n = 0; n < N; ++n) {
+    if (m.unit_ok && m.t == ((s + n) & (m.lh - 1))) {
+      Staged<A>* slot = wst + (s + n) * m.uw_count + m.uw;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) slot->w[c] = G[n][c];
+    }
+  }
+}
+
+// A location gradient pair: one 4-byte store for 16-bit locations (grad_loc is
+// 4-byte aligned), else one store per coordinate.
+template <typename TL, typename A>
+__device__ inline void store_loc_pair(TL* p, A x, A y) {
+  if constexpr (sizeof(TL) == 2) {
+    *reinterpret_cast<uint32_t*>(p) = Chan16<TL, 2>::pack(x, y);
+  } else {
+    store_elem(p, x);
+    store_elem(p + 1, y);
+  }
+}
+
 // Location and weight gradients, sample-parallel, laid out like the forward.
 template <typename T, typename TL, int CV, bool SOFTMAX>
 __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_kernel(const Problem p) {
@@ -2241,11 +2355,14 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
   const int LP = p.L * p.P;
   Staged<A>* wst = reinterpret_cast<Staged<A>*>(smem + sizeof(Level) * p.L) +
                    m.wave * m.uw_count * LP;
+  const size_t raw_at =
+      (sizeof(Level) * p.L + sizeof(Staged<A>) * (blockDim.x / kWave) * m.uw_count * LP + 15) & ~size_t(15);
+  const UnitRaw raw = copy_unit_records<T, TL>(p, m, smem + raw_at);
 
   load_levels(p, levels);
   __syncthreads();
   A smax, sinv;
-  stage_samples<T, TL, SOFTMAX>(p, m, levels, wst, smax, sinv);
+  stage_samples<T, TL, SOFTMAX>(p, m, levels, raw, wst, smax, sinv);
   __syncthreads();
 
   // Gather the corners and form G_c; the lane that staged sample s keeps its G_c
@@ -2256,28 +2373,14 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
   const uint32_t lane_bytes = uint32_t(m.t * CV * ES);
   R g{};
   if (lane_ok) g = *reinterpret_cast<const R*>(p.grad_out + (m.gunit * p.D + m.t * CV) * ES);
-  for (int s = 0; s < LP; ++s) {
-    Staged<A>* slot = wst + s * m.uw_count + m.uw;
-    const Staged<A> st = *slot;
-    A G[4] = {A(0), A(0), A(0), A(0)};
-    if (lane_ok) {
-      R v[4];
-#pragma unroll
-      for (int c = 0; c < 4; ++c) v[c] = *reinterpret_cast<const R*>(img + (st.off[c] + lane_bytes));
-#pragma unroll
-      for (int c = 0; c < 4; ++c) G[c] = Chan<T, CV>::dot(g, v[c], G[c]);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; ++c) G[c] = unit_sum(G[c], m.lh);
-    if (m.unit_ok && m.t == (s & (m.lh - 1))) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) slot->w[c] = G[c];
-    }
-  }
+  int s = 0;
+  for (; s + kSampleBatch <= LP; s += kSampleBatch)
+    corner_dots<T, CV, kSampleBatch>(m, wst, s, lane_ok, img, lane_bytes, g);
+  for (; s < LP; ++s) corner_dots<T, CV, 1>(m, wst, s, lane_ok, img, lane_bytes, g);
 
   // Per-sample location and weight gradients by the lane that staged the sample.
-  const TL* loc = reinterpret_cast<const TL*>(p.loc) + m.gunit * LP * 2;
-  const T* attn = reinterpret_cast<const T*>(p.attn) + m.gunit * LP;
+  const TL* loc = reinterpret_cast<const TL*>(raw.loc);
+  const T* attn = reinterpret_cast<const T*>(raw.attn);
   TL* gloc = reinterpret_cast<TL*>(p.grad_loc) + m.gunit * LP * 2;
   T* gattn = reinterpret_cast<T*>(p.grad_attn) + m.gunit * LP;
   const uint32_t pos_bytes = uint32_t(p.H * p.D * ES);
@@ -2299,8 +2402,7 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
       const A gpv = ge.w00 * G00 + ge.w01 * G01 + ge.w10 * G10 + ge.w11 * G11;
       const A gx = a * A(lv.w) * ((one - ge.dy) * (G01 - G00) + ge.dy * (G11 - G10));
       const A gy = a * A(lv.h) * ((one - ge.dx) * (G10 - G00) + ge.dx * (G11 - G01));
-      store_elem(gloc + 2 * s, gx);
-      store_elem(gloc + 2 * s + 1, gy);
+      store_loc_pair(gloc + 2 * s, gx, gy);
       if constexpr (SOFTMAX) {
         dot += a * gpv;
         slot->w[0] = gpv;
@@ -2381,7 +2483,7 @@ bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) 
 
 // Choose the channel width, the unit width and the workgroup size.
 int make_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, int64_t L,
-              int64_t P, bool backward, const void* const* vec_ptrs, int n_vec, Plan* plan) {
+              int64_t P, bool backward, const void* const* vec_ptrs, int n_vec, Plan* plan, int loc_es) {
   const int es = elem_size(dtype);
   if (es == 0) return fail(MSDA_ERR_INVALID, "msda: unknown value dtype code %d", dtype);
   if (B < 0 || S < 0 || H < 0 || D < 0 || Q < 0 || L < 0 || P < 0)
@@ -2419,19 +2521,22 @@ int make_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, 
   const size_t staged = (dtype == MSDA_F64)             ? sizeof(Staged<double>)
                         : (!backward && es == 2 && cv >= 2) ? sizeof(StagedPk)
                                                             : sizeof(Staged<float>);
+  // Per wave: the staged records, and the LDS copy of the units' locations and weights.
+  const size_t raw_wave = size_t(unit_raw_bytes(uw, int(L * P), loc_es, es));
   const size_t per_wave = size_t(uw) * size_t(L * P) * staged;
   const size_t levels_bytes = sizeof(Level) * size_t(L);
-  if (levels_bytes + per_wave > kMaxLds)
+  auto lds_of = [&](int w) { return ((levels_bytes + per_wave * w + 15) & ~size_t(15)) + raw_wave * w; };
+  if (lds_of(1) > kMaxLds)
     return fail(MSDA_ERR_UNSUPPORTED,
                 "msda: %lld samples per (query, head) do not fit the %zu-byte LDS staging of one "
                 "wave (%zu bytes needed)",
-                (long long)(L * P), kMaxLds, levels_bytes + per_wave);
+                (long long)(L * P), kMaxLds, lds_of(1));
   const int64_t units = Q * H;
   int waves = kMaxWavesPerBlock;
   // Fewer waves per workgroup when the grid would leave CUs idle or LDS is short.
   while (waves > 1) {
     const int64_t blocks = B * ((units + int64_t(waves) * uw - 1) / (int64_t(waves) * uw));
-    if (levels_bytes + per_wave * waves <= kMaxLds && blocks >= 2048) break;
+    if (lds_of(waves) <= kMaxLds && blocks >= 2048) break;
     waves >>= 1;
   }
   plan->cv = cv;
@@ -2440,7 +2545,7 @@ int make_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, 
   plan->units_per_block = waves * uw;
   plan->blocks_per_batch = int((units + plan->units_per_block - 1) / plan->units_per_block);
   plan->num_blocks = B * plan->blocks_per_batch;
-  plan->lds = levels_bytes + per_wave * waves;
+  plan->lds = lds_of(waves);
   if (plan->num_blocks * kWave * waves >= (int64_t(1) << 32) || plan->num_blocks >= kInt32)
     return fail(MSDA_ERR_UNSUPPORTED, "msda: launch grid too large (%lld workgroups)",
                 (long long)plan->num_blocks);
@@ -2530,7 +2635,7 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
                        const void* grad_attn, size_t lds_limit, int cus, BackwardPlan* plan) {
   // vec_ptrs: value, grad_output, grad_value (channel vectors), then the locations.
   const int n_chan = std::min(n_vec, 3);
-  int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_chan, &plan->sample);
+  int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_chan, &plan->sample, elem_size(loc_dtype));
   if (rc != MSDA_OK) return rc;
   const int es = elem_size(dtype);
   // Channels per register item: the widest power of two that divides D, fits a
@@ -2763,6 +2868,14 @@ int zero_fill(void* ptr, int64_t bytes, hipStream_t stream, const char* who) {
   return MSDA_OK;
 }
 
+// The widest piece (16, 8, 4, 2 or 1 bytes) that divides a unit's bytes and the
+// alignment of ptr, for the LDS copy of a wave's locations or weights.
+int copy_piece(int64_t unit_bytes, const void* ptr) {
+  for (int pc = 16; pc > 1; pc >>= 1)
+    if (unit_bytes % pc == 0 && aligned(ptr, pc)) return pc;
+  return 1;
+}
+
 Problem make_problem(const void* value, const void* shapes, const void* starts, int index_dtype,
                      const void* loc, const void* attn, int64_t B, int64_t S, int64_t H, int64_t D,
                      int64_t Q, int64_t L, int64_t P, const Plan& plan) {
@@ -2817,7 +2930,7 @@ int msda_launch_geometry(int value_dtype, int64_t batch, int64_t spatial, int64_
   }
   Plan plan;
   const int rc = make_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
-                           false, nullptr, 0, &plan);
+                           false, nullptr, 0, &plan, elem_size(value_dtype));
   if (rc != MSDA_OK) return rc;
   if (channels_per_lane) *channels_per_lane = plan.cv;
   if (lanes_per_unit) *lanes_per_unit = 1 << plan.lh_log2;
@@ -2847,11 +2960,13 @@ int msda_forward(const void* value, int value_dtype, const void* spatial_shapes,
   const void* vec[] = {value, output};
   Plan plan;
   rc = make_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points, false,
-                 vec, 2, &plan);
+                 vec, 2, &plan, elem_size(loc_dtype));
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,
                            channels, queries, levels, points, plan);
+  p.loc_piece = copy_piece(levels * points * 2 * elem_size(loc_dtype), sampling_locations);
+  p.attn_piece = copy_piece(levels * points * elem_size(value_dtype), attention_weights);
   p.out = static_cast<char*>(output);
   const bool softmax = flags & MSDA_SOFTMAX;
   const hipError_t err = dispatch(
@@ -2916,6 +3031,8 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,
                            channels, queries, levels, points, plan.sample);
+  p.loc_piece = copy_piece(levels * points * 2 * elem_size(loc_dtype), sampling_locations);
+  p.attn_piece = copy_piece(levels * points * elem_size(value_dtype), attention_weights);
   p.grad_out = static_cast<const char*>(grad_output);
   p.grad_value = static_cast<char*>(grad_value);
   p.grad_loc = static_cast<char*>(grad_sampling_locations);
