@@ -977,6 +977,32 @@ __device__ inline int sample_key(A lx, A ly, const Level& lv, const LevelTiles& 
   return in ? bucket_key(t, int(floor(x)), int(floor(y)), lv) : -1;
 }
 
+// Slots for the four samples of a group (points p .. p + 3 of one query and level)
+// from the bucket cursors `cur`: samples that share a bucket get consecutive slots
+// from one atomic, so a tile's candidate list holds a query's points of one level
+// side by side, and the grad_value kernel's lanes then read the same grad_out row
+// and location line together. Keys < 0 get no slot.
+template <typename Cursor>
+__device__ inline void group_slots(const int (&key)[4], Cursor* cur, int (&slot)[4]) {
+#pragma unroll
+  for (int c = 0; c < 4; ++c) slot[c] = -1;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    bool first = key[c] >= 0;
+#pragma unroll
+    for (int d = 0; d < c; ++d) first = first && key[d] != key[c];
+    if (first) {
+      int n = 0;
+#pragma unroll
+      for (int d = c; d < 4; ++d) n += key[d] == key[c] ? 1 : 0;
+      int at = atomicAdd(&cur[key[c]], n);
+#pragma unroll
+      for (int d = c; d < 4; ++d)
+        if (key[d] == key[c]) slot[d] = at++;
+    }
+  }
+}
+
 template <int N> struct KeyWord;
 template <> struct KeyWord<2> { using type = u32x2_v; };  // four 16-bit keys
 template <> struct KeyWord<4> { using type = u32x4_v; };  // four 32-bit keys
@@ -1089,11 +1115,16 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
         keys_of(g, key);
         save(g, key);
       }
+      if constexpr (PLACE) {
+        int slot[4];
+        group_slots(key, bucket_row, slot);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        if (key[c] < 0) continue;
-        const int at = atomicAdd(&bucket_row[key[c]], 1);
-        if constexpr (PLACE) out[at] = uint32_t(4 * g + c);
+        for (int c = 0; c < 4; ++c)
+          if (key[c] >= 0) out[slot[c]] = uint32_t(4 * g + c);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (key[c] >= 0) atomicAdd(&bucket_row[key[c]], 1);
       }
     }
     return;
@@ -1135,9 +1166,11 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
 #pragma unroll
     for (int i = 0; i < kGroups; ++i) {
       const int64_t g = g0 + int64_t(i) * kBucketThreads + threadIdx.x;
+      int slot[4];
+      group_slots(key[i], hist, slot);
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        if (key[i][c] >= 0) out[atomicAdd(&hist[key[i][c]], 1)] = uint32_t(4 * g + c);
+        if (key[i][c] >= 0) out[slot[c]] = uint32_t(4 * g + c);
     }
   }
 }
