@@ -736,6 +736,10 @@ struct BwdGeom {
   FastDiv div_gpl;  // by P / 4, groups per level
   int key_bytes;    // 2 or 4: the count pass saves every sample's key in the grad_value
                     // scratch for the place pass; 0: the place pass recomputes them
+  int chunks;       // > 0: the grouped passes may keep per-workgroup counts (chunk_counts,
+                    // `chunks` workgroups per (b, h)) for the scan to turn into
+                    // per-workgroup bucket offsets, with no global atomics and no clear;
+                    // every kernel decides the same way with chunked_sort()
 };
 
 struct LevelTiles {
@@ -868,6 +872,26 @@ __device__ inline int64_t load_tiles(const Problem& p, const BwdGeom& bg, Level*
   if (threadIdx.x == 0) *total_out = plan_tiles(p, bg, levels, lt);
   __syncthreads();
   return *total_out;
+}
+
+// The per-workgroup count rows of the chunked bucket sort, nkeys ints for each
+// (b, h, workgroup), after the bucket rows and the matrix-core kernel's queue
+// counters; then the bucket totals, nkeys ints per (b, h).
+__device__ inline int* chunk_counts(int* buckets, const Problem& p, int64_t nkeys) {
+  return buckets + ((int64_t(p.B) * p.H * nkeys + 31) & ~int64_t(31)) + kQueueInts;
+}
+__device__ inline int* chunk_totals(int* buckets, const Problem& p, const BwdGeom& bg, int64_t nkeys) {
+  return chunk_counts(buckets, p, nkeys) + int64_t(p.B) * p.H * bg.chunks * nkeys;
+}
+
+// Whether the bucket sort keeps per-workgroup counts, from the device's tile count:
+// every bucket fits the bucketing kernels' LDS counters, and the scratch holds the
+// bucket rows, the queue counters and the count rows.
+__device__ inline bool chunked_sort(const Problem& p, const BwdGeom& bg, int64_t nkeys) {
+  if (bg.chunks <= 0 || nkeys > bg.keys_lds) return false;
+  const int64_t bh = int64_t(p.B) * p.H;
+  const int64_t need = ((bh * nkeys + 31) & ~int64_t(31)) + kQueueInts + bh * (bg.chunks + 1) * nkeys;
+  return need <= bh * bg.keys_alloc;
 }
 
 // Counting (PLACE = false) or placing (PLACE = true) pass of the bucket sort.
@@ -1023,6 +1047,7 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
   using A = typename Elem<TL>::acc;
   using Word = typename KeyWord<KB>::type;
   constexpr int kGroups = kBucketSamples / 4;  // groups per thread
+  __shared__ int scan_sums[kBucketThreads / kWave];
   extern __shared__ __align__(16) unsigned char smem[];
   Level* levels = reinterpret_cast<Level*>(smem);
   LevelTiles* lt = reinterpret_cast<LevelTiles*>(smem + sizeof(Level) * size_t(p.L));
@@ -1143,24 +1168,53 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
         if (key[c] >= 0) atomicAdd(&hist[key[c]], 1);
     }
     __syncthreads();
-    for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) {
-      const int c = hist[k];
-      if (c > 0) atomicAdd(&bucket_row[k], c);
+    if (chunked_sort(p, bg, nkeys)) {
+      // Every count of this workgroup, zeros included, for the scan.
+      int* row = chunk_counts(buckets, p, nkeys) + (int64_t(bh) * chunks_per_bh + chunk) * nkeys;
+      for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) row[k] = hist[k];
+    } else {
+      for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) {
+        const int c = hist[k];
+        if (c > 0) atomicAdd(&bucket_row[k], c);
+      }
     }
   } else {
-    // Counts again (from the saved keys), then this workgroup's range of every bucket.
     int key[kGroups][4];
 #pragma unroll
-    for (int i = 0; i < kGroups; ++i) {
-      restore(g0 + int64_t(i) * kBucketThreads + threadIdx.x, key[i]);
+    for (int i = 0; i < kGroups; ++i) restore(g0 + int64_t(i) * kBucketThreads + threadIdx.x, key[i]);
+    if (chunked_sort(p, bg, nkeys)) {
+      // This workgroup's offset in every bucket: the bucket's start (an exclusive
+      // scan of the totals, here in LDS) plus the counts of the workgroups before it
+      // (from the scan kernel). Workgroup 0 of each (b, h) writes the bucket ends.
+      const int* tot = chunk_totals(buckets, p, bg, nkeys) + int64_t(bh) * nkeys;
+      for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) hist[k] = tot[k];
+      __syncthreads();
+      int carry = 0;
+      for (int64_t k0 = 0; k0 < nkeys; k0 += kBucketThreads) {
+        const int64_t k = k0 + threadIdx.x;
+        const int v = k < nkeys ? hist[k] : 0;
+        int sum;
+        const int ex = block_exclusive_scan(v, scan_sums, &sum);
+        if (k < nkeys) {
+          hist[k] = carry + ex;
+          if (chunk == 0) bucket_row[k] = carry + ex + v;
+        }
+        carry += sum;
+      }
+      const int* row = chunk_counts(buckets, p, nkeys) + (int64_t(bh) * chunks_per_bh + chunk) * nkeys;
+      for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) hist[k] += row[k];
+    } else {
+      // Counts again (from the saved keys), then this workgroup's range of every bucket.
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        if (key[i][c] >= 0) atomicAdd(&hist[key[i][c]], 1);
-    }
-    __syncthreads();
-    for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) {
-      const int c = hist[k];
-      if (c > 0) hist[k] = atomicAdd(&bucket_row[k], c);  // this workgroup's cursor in bucket k
+      for (int i = 0; i < kGroups; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (key[i][c] >= 0) atomicAdd(&hist[key[i][c]], 1);
+      __syncthreads();
+      for (int64_t k = threadIdx.x; k < nkeys; k += kBucketThreads) {
+        const int c = hist[k];
+        if (c > 0) hist[k] = atomicAdd(&bucket_row[k], c);  // this workgroup's cursor in bucket k
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -1175,13 +1229,17 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
   }
 }
 
-// Counts to exclusive offsets, one workgroup per (b, h).
-__global__ __launch_bounds__(1024) void msda_bucket_scan_kernel(const Problem p, const BwdGeom bg,
-                                                                int* __restrict__ buckets) {
+// Counts to exclusive offsets. Unchunked: workgroup (b, h) < B H scans row (b, h).
+// Chunked: thread (b, h, bucket) turns the bucket's per-workgroup counts into the
+// counts of the workgroups before each (in place) and writes the bucket total; the
+// place pass scans the totals. Workgroup 0 then also clears the matrix-core kernel's
+// queue counters.
+__global__ __launch_bounds__(256) void msda_bucket_scan_kernel(const Problem p, const BwdGeom bg,
+                                                               int* __restrict__ buckets, int chunks_per_bh) {
   __shared__ Level levels_s[kMaxOrderedLevels];
   __shared__ LevelTiles lt_s[kMaxOrderedLevels];
   __shared__ int64_t total_s[2];
-  __shared__ int wave_sums[1024 / kWave];
+  __shared__ int wave_sums[256 / kWave];
   extern __shared__ __align__(16) unsigned char smem[];
   Level* levels = p.L <= kMaxOrderedLevels ? levels_s : reinterpret_cast<Level*>(smem);
   LevelTiles* lt = p.L <= kMaxOrderedLevels ? lt_s
@@ -1189,6 +1247,31 @@ __global__ __launch_bounds__(1024) void msda_bucket_scan_kernel(const Problem p,
   const int64_t ntiles = load_tiles(p, bg, levels, lt, total_s);
   const int64_t nkeys = 4 * ntiles;
   if (ntiles < 0 || nkeys > bg.keys_alloc) return;
+  const int64_t nbh = int64_t(p.B) * p.H;
+  if (chunked_sort(p, bg, nkeys)) {
+    if (blockIdx.x == 0)
+      for (int i = threadIdx.x; i < kQueueInts; i += blockDim.x) buckets[nbh * nkeys + i] = 0;
+    for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < nbh * nkeys;
+         i += int64_t(gridDim.x) * blockDim.x) {
+      const int64_t bh = i / nkeys, k = i - bh * nkeys;
+      int* cnt = chunk_counts(buckets, p, nkeys) + bh * chunks_per_bh * nkeys + k;
+      constexpr int kBatch = 8;  // rows loaded together
+      int run = 0;
+      for (int c0 = 0; c0 < chunks_per_bh; c0 += kBatch) {
+        int v[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) v[u] = c0 + u < chunks_per_bh ? cnt[int64_t(c0 + u) * nkeys] : 0;
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          if (c0 + u < chunks_per_bh) cnt[int64_t(c0 + u) * nkeys] = run;
+          run += v[u];
+        }
+      }
+      chunk_totals(buckets, p, bg, nkeys)[i] = run;
+    }
+    return;
+  }
+  if (blockIdx.x >= nbh) return;
   int* row = buckets + int64_t(blockIdx.x) * nkeys;
   int carry = 0;
   for (int64_t k0 = 0; k0 < nkeys; k0 += blockDim.x) {
@@ -1215,6 +1298,7 @@ __global__ __launch_bounds__(256) void msda_bucket_clear_kernel(const Problem p,
   const int64_t ntiles = load_tiles(p, bg, levels, lt, total_s);
   const int64_t nkeys = 4 * ntiles;
   if (ntiles < 0 || nkeys > bg.keys_alloc) return;
+  if (chunked_sort(p, bg, nkeys)) return;  // the passes write every count; the scan clears the queues
   // The matrix-core grad_value keeps its work-queue counters right after the rows.
   const int64_t n = int64_t(p.B) * p.H * nkeys + (bg.sub_log2 > 0 ? kQueueInts : 0);
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
@@ -2626,6 +2710,7 @@ struct BackwardPlan {
   size_t bucket_lds;
   int64_t bucket_chunks;  // bucketing workgroups per (b, h)
   int64_t zero_keys;      // bucket counters to clear per (b, h), at most
+  int64_t scan_blocks;    // workgroups of msda_bucket_scan_kernel
   bool mfma;              // grad_value on the matrix cores (4 x 4 tiles)
   int mfma_nb;            // 16-channel column blocks
   int64_t mfma_blocks;
@@ -2756,6 +2841,11 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   bg.key_bytes = 4 * tiles_bound < 0xffff ? 2 : 4;
   if (B * H * samples_bh * bg.key_bytes > B * S * H * D * es) bg.group4 = 0;
   if (!bg.group4) bg.key_bytes = 0;
+  // Per-workgroup counts for the grouped passes, where the device finds them room.
+  bg.chunks = bg.group4 ? int(plan->bucket_chunks) : 0;
+  plan->scan_blocks = B * H;
+  if (bg.chunks > 0)  // a grid-stride loop over (b, h, bucket) when chunked
+    plan->scan_blocks = std::max<int64_t>(plan->scan_blocks, std::min<int64_t>((B * H * plan->zero_keys + 255) / 256, 512));
   if (bg.group4) {
     bg.div_gpq = make_fastdiv(uint32_t(L * P / 4));
     bg.div_gpl = make_fastdiv(uint32_t(P / 4));
@@ -2840,8 +2930,8 @@ hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* bucke
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(count, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
                          int(plan.bucket_chunks));
-      hipLaunchKernelGGL(msda_bucket_scan_kernel, dim3(unsigned(p.B * p.H)), dim3(1024), scan_lds, st, p,
-                         plan.bg, buckets);
+      hipLaunchKernelGGL(msda_bucket_scan_kernel, dim3(unsigned(plan.scan_blocks)), dim3(256), scan_lds, st, p,
+                         plan.bg, buckets, int(plan.bucket_chunks));
       hipLaunchKernelGGL(place, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
                          int(plan.bucket_chunks));
       return hipGetLastError();
@@ -2856,8 +2946,8 @@ hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* bucke
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(count, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
                      int(plan.bucket_chunks));
-  hipLaunchKernelGGL(msda_bucket_scan_kernel, dim3(unsigned(p.B * p.H)), dim3(1024), scan_lds, st, p,
-                     plan.bg, buckets);
+  hipLaunchKernelGGL(msda_bucket_scan_kernel, dim3(unsigned(plan.scan_blocks)), dim3(256), scan_lds, st, p,
+                     plan.bg, buckets, int(plan.bucket_chunks));
   hipLaunchKernelGGL(place, grid, block, plan.bucket_lds, st, p, plan.bg, buckets, entries,
                      int(plan.bucket_chunks));
   return hipGetLastError();
