@@ -2842,7 +2842,7 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   if (B * H * samples_bh * bg.key_bytes > B * S * H * D * es) bg.group4 = 0;
   if (!bg.group4) bg.key_bytes = 0;
   // Per-workgroup counts for the grouped passes, where the device finds them room.
-  bg.chunks = bg.group4 ? int(plan->bucket_chunks) : 0;
+  bg.chunks = bg.group4 && getenv("DEFORMOPS_AMD_ATOMIC_SORT") == nullptr ? int(plan->bucket_chunks) : 0;
   plan->scan_blocks = B * H;
   if (bg.chunks > 0)  // a grid-stride loop over (b, h, bucket) when chunked
     plan->scan_blocks = std::max<int64_t>(plan->scan_blocks, std::min<int64_t>((B * H * plan->zero_keys + 255) / 256, 512));

@@ -140,17 +140,23 @@ def test_shapes_match_oracle(device, levels, B, Q, H, D, P, dtype):
 
 # The two grad_value kernels for 16-bit dtypes: the matrix-core one (the default for
 # D = 16, 32, 48, 64) and the VALU owner kernel (every other case, and the fallback
-# when the bucket scratch is short), selected by DEFORMOPS_AMD_NO_MFMA.
+# when the bucket scratch is short), selected by DEFORMOPS_AMD_NO_MFMA; and the two
+# ways the bucket sort publishes its counts: per-workgroup count rows (the default
+# where the scratch has room) or global atomics, forced by DEFORMOPS_AMD_ATOMIC_SORT.
 
 
-@pytest.mark.parametrize("path", ["mfma", "valu"])
+@pytest.mark.parametrize("path", ["mfma", "mfma-atomic-sort", "valu", "valu-atomic-sort"])
 @pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
 @pytest.mark.parametrize("cfg", [2, 3])
 def test_grad_value_paths_match_oracle(device, monkeypatch, cfg, dtype, path):
-    if path == "valu":
+    if path.startswith("valu"):
         monkeypatch.setenv("DEFORMOPS_AMD_NO_MFMA", "1")
     else:
         monkeypatch.delenv("DEFORMOPS_AMD_NO_MFMA", raising=False)
+    if path.endswith("atomic-sort"):
+        monkeypatch.setenv("DEFORMOPS_AMD_ATOMIC_SORT", "1")
+    else:
+        monkeypatch.delenv("DEFORMOPS_AMD_ATOMIC_SORT", raising=False)
     w = make_workload(cfg).to(device, dtype)
     for softmax in (False, True):
         check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
