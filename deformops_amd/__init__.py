@@ -11,11 +11,11 @@ from __future__ import annotations
 
 from .version import __version__
 
-__all__ = ["__version__", "registry"]
+__all__ = ["__version__", "nn", "registry"]
 
 
 def __getattr__(name: str):
-    if name in ("registry", "core"):
+    if name in ("registry", "core", "nn"):
         import importlib  # noqa: PLC0415
 
         return importlib.import_module(f".{name}", __name__)

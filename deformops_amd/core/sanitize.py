@@ -22,6 +22,7 @@ if TYPE_CHECKING:
 
 __all__ = [
     "VALIDATE_ENV_VAR",
+    "check_2power",
     "check_divisible",
     "check_msda_call",
     "check_msda_params",
@@ -57,6 +58,17 @@ def check_divisible(a: int, b: int) -> None:
         raise ValueError(msg)
     if a % b != 0:
         msg = f"Expected {a} to be divisible by {b}"
+        raise ValueError(msg)
+
+
+def check_2power(n: int) -> None:
+    """Raise ``ValueError`` unless ``n`` is a positive power of two (reference
+    ``core/sanitize.py:56-74``)."""
+    if n <= 0:
+        msg = f"Expected a positive integer, got: {n}"
+        raise ValueError(msg)
+    if n & (n - 1):
+        msg = f"Expected a power of 2, got: {n}"
         raise ValueError(msg)
 
 
