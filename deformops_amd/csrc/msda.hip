@@ -2185,6 +2185,23 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
   unsigned char* wt = gst + kMfmaK * 32 * NB;                // four weight tiles
 
   const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
+  if (!accumulate) {
+    // grad_value at positions no valid level covers is zero (the tiles own all the
+    // others, so this never meets their stores).
+    const int64_t n = int64_t(p.B) * p.S;
+    for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + tid; idx < n; idx += int64_t(gridDim.x) * blockDim.x) {
+      const int pos = int(idx % p.S);
+      bool covered = false;
+      for (int l = 0; l < p.L && !covered; ++l) {
+        const Level lv = levels[l];
+        covered = lv.ok && pos >= lv.start && int64_t(pos) < int64_t(lv.start) + int64_t(lv.h) * lv.w;
+      }
+      if (!covered) {
+        T* dst = reinterpret_cast<T*>(p.grad_value) + idx * p.H * D;
+        for (int i = 0; i < p.H * D; ++i) store_elem(dst + i, 0.f);
+      }
+    }
+  }
   if (ntiles <= 0 || 4 * ntiles > bg.keys_alloc) return;  // the host launches this only when bucketed
   if (tid == 0) {
     order_levels(p, levels, lt, order, rank_base);
@@ -3173,7 +3190,7 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
           e = launch_buckets<TL>(plan, p, buckets, entries, st);
           if (e != hipSuccess) return e;
         }
-        if (!accumulate) {
+        if (!accumulate && !plan.mfma) {  // the matrix-core kernel zeroes the gaps itself
           const int64_t n = int64_t(p.B) * p.S;
           hipLaunchKernelGGL((msda_gap_zero_kernel<T>), dim3(unsigned((n + 255) / 256)), dim3(256),
                              sizeof(Level) * size_t(p.L), st, p);

@@ -390,6 +390,22 @@ def test_malformed_level_table_reads_nothing_out_of_bounds(device):
     assert rel_err(out, ref) <= 1e-5
 
 
+@pytest.mark.parametrize("dtype", [BF16, F16, F32], ids=["bf16", "f16", "f32"])
+def test_positions_outside_every_level_get_zero_gradient(device, dtype):
+    """value rows that no level covers (a gap between the levels and a tail) get
+    exactly zero in grad_value, which the kernels allocate uninitialized."""
+    w = make_workload(0, levels=((8, 8), (4, 4)), batch=2, queries=30, heads=2, channels=32)
+    B, S, H, D, Q, L, P = w.sizes
+    starts = torch.tensor([0, 70])
+    value = torch.randn(B, 90, H, D, generator=torch.Generator().manual_seed(5), dtype=torch.float64)
+    w = dataclasses.replace(w, value=value, level_start_index=starts).to(device, dtype)
+    for softmax in (False, True):
+        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                             label="gaps")
+        _, gv, _, _ = run_hip(*w.operands(softmax=softmax), w.grad_output, softmax=softmax)
+        assert torch.count_nonzero(gv[:, 64:70]) == 0 and torch.count_nonzero(gv[:, 86:]) == 0
+
+
 # Precision of the 16-bit gradients: fp32 sums rounded once, so no drift.
 
 
