@@ -894,6 +894,27 @@ __device__ inline bool chunked_sort(const Problem& p, const BwdGeom& bg, int64_t
   return need <= bh * bg.keys_alloc;
 }
 
+// Per-unit softmax statistics for the grad_value kernels: the max and the sum of
+// exp(logit - max) of every (b, q, h), written by msda_softmax_stats_kernel after
+// the place pass (over the per-workgroup counts, done with by then), where the
+// scratch has room. A candidate's weight is then exp(logit - max) / sum: one logit
+// and one statistics load instead of a pass over the unit's L * P logits.
+template <typename A> struct SoftStat {
+  A mx, sum;
+};
+template <typename A>
+__device__ inline SoftStat<A>* softmax_stats(int* buckets, const Problem& p, int64_t nkeys) {
+  return reinterpret_cast<SoftStat<A>*>(chunk_counts(buckets, p, nkeys));
+}
+template <typename A>
+__device__ inline bool softmax_stats_fit(const Problem& p, const BwdGeom& bg, int64_t nkeys, const int* buckets) {
+  const int64_t bh = int64_t(p.B) * p.H;
+  const int64_t ints = int64_t(sizeof(SoftStat<A>) / sizeof(int)) * bh * p.Q;
+  const int64_t need = ((bh * nkeys + 31) & ~int64_t(31)) + kQueueInts + ints;
+  const uintptr_t at = reinterpret_cast<uintptr_t>(softmax_stats<A>(const_cast<int*>(buckets), p, nkeys));
+  return need <= bh * bg.keys_alloc && at % alignof(SoftStat<A>) == 0;
+}
+
 // Counting (PLACE = false) or placing (PLACE = true) pass of the bucket sort.
 // Workgroup: kBucketThreads * kBucketSamples consecutive samples (q, l, p) of one
 // (b, h). `buckets` holds one counter per bucket and (b, h): counts after the count
@@ -1305,6 +1326,34 @@ __global__ __launch_bounds__(256) void msda_bucket_clear_kernel(const Problem p,
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) buckets[i] = 0;
 }
 
+// The per-unit softmax statistics (see SoftStat), one thread per (b, q, h).
+template <typename T>
+__global__ __launch_bounds__(256) void msda_softmax_stats_kernel(const Problem p, const BwdGeom bg,
+                                                                  int* __restrict__ buckets) {
+  using A = typename Elem<T>::acc;
+  __shared__ Level levels_s[kMaxOrderedLevels];
+  __shared__ LevelTiles lt_s[kMaxOrderedLevels];
+  __shared__ int64_t total_s[2];
+  extern __shared__ __align__(16) unsigned char smem[];
+  Level* levels = p.L <= kMaxOrderedLevels ? levels_s : reinterpret_cast<Level*>(smem);
+  LevelTiles* lt = p.L <= kMaxOrderedLevels ? lt_s
+                                             : reinterpret_cast<LevelTiles*>(smem + sizeof(Level) * size_t(p.L));
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total_s);
+  const int64_t nkeys = 4 * ntiles;
+  if (ntiles < 0 || nkeys > bg.keys_alloc || !softmax_stats_fit<A>(p, bg, nkeys, buckets)) return;
+  SoftStat<A>* st = softmax_stats<A>(buckets, p, nkeys);
+  const int LP = p.L * p.P;
+  const int64_t units = int64_t(p.B) * p.Q * p.H;
+  for (int64_t u = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; u < units; u += int64_t(gridDim.x) * blockDim.x) {
+    const T* lg = reinterpret_cast<const T*>(p.attn) + u * LP;
+    A mx = -INFINITY;
+    for (int i = 0; i < LP; ++i) mx = fmax(mx, load_acc(lg + i));
+    A sum(0);
+    for (int i = 0; i < LP; ++i) sum += exp_acc(load_acc(lg + i) - mx);
+    st[u] = SoftStat<A>{mx, sum};
+  }
+}
+
 // Zeroes grad_value[b, pos, :, :] at every position no valid level covers; the tile
 // owners write all the others.
 template <typename T>
@@ -1505,6 +1554,9 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
   const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
   if (ntiles <= 0) return;
   const bool bucketed = 4 * ntiles <= bg.keys_alloc;
+  const SoftStat<A>* stats = SOFTMAX && bucketed && softmax_stats_fit<A>(p, bg, 4 * ntiles, buckets)
+                                 ? softmax_stats<A>(const_cast<int*>(buckets), p, 4 * ntiles)
+                                 : nullptr;
   if (tid == 0) {
     order_levels(p, levels, lt, order, rank_base);
     for (int i = 0; i < cap; ++i) cnt[i] = 0;
@@ -1657,7 +1709,13 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
         A a;
         if constexpr (SOFTMAX) {
           const uint32_t q = fdiv(c_own, bg.div_lp), s = c_own - q * uint32_t(LP);
-          a = unit_weight<T, true>(attn_all + (unit0 + int64_t(q) * p.H) * LP, LP, int(s));
+          const int64_t u = unit0 + int64_t(q) * p.H;
+          if (stats) {
+            const SoftStat<A> st = stats[u];
+            a = exp_acc(load_acc(attn_all + u * LP + s) - st.mx) / st.sum;
+          } else {
+            a = unit_weight<T, true>(attn_all + u * LP, LP, int(s));
+          }
         } else {
           a = to_acc(c_attn);
         }
@@ -1886,7 +1944,8 @@ __device__ inline uint32_t cand_entry(const uint32_t* __restrict__ ent, const Ca
 // the previous block has staged its rows).
 template <typename T, typename TL> struct MfmaMeta {
   LocPair<TL> loc;
-  T attn;
+  T attn;              // the weight, or with softmax the logit
+  SoftStat<float> st;  // softmax: the unit's statistics (when stats are kept)
 };
 template <int NB> struct MfmaRows {
   u32x4_v piece[2 * NB];
@@ -1902,13 +1961,17 @@ struct MfmaTile {
   uint32_t ncand;
   FastDiv div_lp;
   int LP;
+  const SoftStat<float>* stats;  // softmax statistics of (b, q = 0, h), stride H per query; or null
+  int H;
 };
 
 template <typename T, typename TL, bool SOFTMAX>
 __device__ inline void mfma_load_meta(const MfmaTile& t, uint32_t e, MfmaMeta<T, TL>& d) {
   const uint32_t q = fdiv(e, t.div_lp), s = e - q * uint32_t(t.LP);
   d.loc = *reinterpret_cast<const LocPair<TL>*>(t.loc + (__umul24(q, t.loc_q) + s * uint32_t(2 * sizeof(TL))));
-  if constexpr (!SOFTMAX) d.attn = *reinterpret_cast<const T*>(t.attn + (__umul24(q, t.attn_q) + s * 2u));
+  if (!SOFTMAX || t.stats) d.attn = *reinterpret_cast<const T*>(t.attn + (__umul24(q, t.attn_q) + s * 2u));
+  if constexpr (SOFTMAX)
+    if (t.stats) d.st = t.stats[__umul24(q, uint32_t(t.H))];
 }
 
 template <int NB>
@@ -1950,8 +2013,12 @@ __device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, 
     const Geom<float> g = geometry<float>(to_acc(d.loc.x), to_acc(d.loc.y), lv, 0u, 1u);
     float a;
     if constexpr (SOFTMAX) {
-      const uint32_t q = fdiv(e, t.div_lp), s = e - q * uint32_t(t.LP);
-      a = unit_weight<T, true>(reinterpret_cast<const T*>(t.attn + __umul24(q, t.attn_q)), t.LP, int(s));
+      if (t.stats) {
+        a = exp_acc(to_acc(d.attn) - d.st.mx) / d.st.sum;
+      } else {
+        const uint32_t q = fdiv(e, t.div_lp), s = e - q * uint32_t(t.LP);
+        a = unit_weight<T, true>(reinterpret_cast<const T*>(t.attn + __umul24(q, t.attn_q)), t.LP, int(s));
+      }
     } else {
       a = to_acc(d.attn);
     }
@@ -2203,6 +2270,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
     }
   }
   if (ntiles <= 0 || 4 * ntiles > bg.keys_alloc) return;  // the host launches this only when bucketed
+  const bool stats_ok = SOFTMAX && softmax_stats_fit<float>(p, bg, 4 * ntiles, buckets);
   if (tid == 0) {
     order_levels(p, levels, lt, order, rank_base);
     // R x R regions, R the power of two nearest the finest level's tile count, at most 16.
@@ -2379,6 +2447,8 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
       t.ncand = cr.ncand;
       t.div_lp = bg.div_lp;
       t.LP = LP;
+      t.H = p.H;
+      t.stats = SOFTMAX && stats_ok ? softmax_stats<float>(buckets, p, 4 * ntiles) + unit0 : nullptr;
 
       f32x4_v acc[4][NB];
       // All K-blocks (per-wave mode), or K-blocks wave, wave + 4, ...
@@ -3189,6 +3259,15 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
         if (plan.bucket) {
           e = launch_buckets<TL>(plan, p, buckets, entries, st);
           if (e != hipSuccess) return e;
+          if (softmax) {  // per-unit softmax statistics, where the scratch has room
+            const int64_t units = int64_t(p.B) * p.Q * p.H;
+            const unsigned blocks = unsigned(std::max<int64_t>(1, std::min<int64_t>((units + 255) / 256, 2048)));
+            const size_t lds = p.L > kMaxOrderedLevels ? (sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) : 0;
+            hipLaunchKernelGGL((msda_softmax_stats_kernel<T>), dim3(blocks), dim3(256), lds, st, p, plan.bg,
+                               buckets);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+          }
         }
         if (!accumulate && !plan.mfma) {  // the matrix-core kernel zeroes the gaps itself
           const int64_t n = int64_t(p.B) * p.S;
