@@ -79,9 +79,10 @@ def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
     """Average device time of each direction alone, through the C ABI, on torch's stream.
 
     The forward is one kernel. The backward call launches the bucket sort of the
-    samples (clear, count, scan, place), the gap zeroing, the owner-computes
-    grad_value kernel and the location / weight gradient kernel, all on this stream;
-    the events bracket the whole call.
+    samples (clear, count, scan, place), the per-unit softmax statistics (softmax
+    only), the owner-computes grad_value kernel (which also zeroes positions no level
+    covers) and the location / weight gradient kernel, all on this stream; the events
+    bracket the whole call.
     """
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
 
@@ -245,7 +246,7 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "msda_backward (C-ABI call: bucket sort, gap zero, grad_value, grad_sample)",
+            "kernel": "msda_backward (C-ABI call: bucket sort, softmax stats if softmax, grad_value, grad_sample)",
             "achieved": round(bwd_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
