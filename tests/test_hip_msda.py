@@ -123,6 +123,10 @@ SHAPES = [
     pytest.param(((10, 12), (5, 6), (3, 3), (2, 2), (1, 1)), 2, 21, 8, 32, 4, id="five-levels"),
     pytest.param(((12, 10), (6, 5)), 1, 13, 1, 256, 2, id="d256"),
     pytest.param(((11, 9), (6, 5), (3, 3)), 2, 19, 3, 48, 4, id="d48"),
+    pytest.param(((9, 11), (5, 6), (3, 3), (2, 2)), 2, 25, 8, 32, 5, id="four-levels-p5"),
+    pytest.param(((8, 8), (4, 4)), 1, 7, 3, 128, 6, id="d128-p6"),
+    pytest.param(((7, 8), (4, 4)), 1, 11, 5, 16, 7, id="odd-heads-p7"),
+    pytest.param(((10, 12), (5, 6), (3, 3), (2, 2), (1, 1)), 1, 9, 2, 64, 8, id="five-levels-p8"),
 ]
 
 
@@ -136,6 +140,29 @@ def test_shapes_match_oracle(device, levels, B, Q, H, D, P, dtype):
     for softmax in (False, True):
         check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
                              label=f"levels={levels} B={B} Q={Q} H={H} D={D} P={P}")
+
+
+# Wider shapes at the size of an encoder (config 2's pyramid, Q = S = 5,376), where
+# the bucket sort and the matrix-core grad_value kernel run as at full size:
+# P not a multiple of 4 (per-sample bucketing), other head widths and head counts,
+# and Deformable DETR's four levels.
+WIDE = [
+    pytest.param({"points": 3}, BF16, id="p3-bf16"),
+    pytest.param({"points": 5}, F16, id="p5-f16"),
+    pytest.param({"channels": 64, "heads": 4}, BF16, id="d64-h4-bf16"),
+    pytest.param({"channels": 16, "heads": 5, "points": 8}, BF16, id="d16-h5-p8-bf16"),
+    pytest.param({"channels": 48, "heads": 3}, F16, id="d48-h3-f16"),
+    pytest.param({"levels": ((64, 64), (32, 32), (16, 16), (8, 8))}, BF16, id="four-levels-bf16"),
+    pytest.param({"points": 6, "heads": 7}, F32, id="p6-h7-f32"),
+]
+
+
+@pytest.mark.parametrize(("sizes", "dtype"), WIDE)
+def test_wider_shapes_at_encoder_size(device, sizes, dtype):
+    w = make_workload(2, **sizes).to(device, dtype)
+    for softmax in (False, True):
+        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                             label=f"config 2 with {sizes}")
 
 
 # The two grad_value kernels for 16-bit dtypes: the matrix-core one (the default for
