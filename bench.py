@@ -13,6 +13,12 @@ restatement of the reference's eager CPU path on a bounded sample of the same
 workload, scaled to one full call.
 
     python bench.py [--steps K] [--warmup W] [--dtype bf16|f16|f32] [--loc-dtype ...]
+                    [--method linear|softmax] [--config 0..4]
+
+``--config`` measures another BASELINE configuration the same way (config 4, the
+headline, is the default and the only one the driver's line is quoted on). The
+``roofline.traffic`` figure is the profiled one of config 4 (bf16, linear) and is
+null for every other workload.
 """
 
 from __future__ import annotations
@@ -126,17 +132,19 @@ def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
     return result
 
 
-def cpu_baseline(dtype: torch.dtype, loc_dtype: torch.dtype, softmax: bool) -> dict:
+def cpu_baseline(config: int, dtype: torch.dtype, loc_dtype: torch.dtype, softmax: bool) -> dict:
     """The reference's eager CPU path (torch restatement) on a bounded sample.
 
-    Sample: batch 1 and the first quarter of config 4's queries (one image's worth,
-    21,504 of the 86,016 (batch, query) pairs), same dtype; 1 warm-up and 3 timed
-    fwd + autograd-bwd iterations, median, scaled x4 to one full call.
+    Sample: batch 1 and at most the first 21,504 queries of the configuration (at
+    config 4, one image: 21,504 of the 86,016 (batch, query) pairs), same dtype;
+    1 warm-up and 3 timed fwd + autograd-bwd iterations, median, scaled by the
+    call's (batch, query) pairs over the sample's.
     """
     from oracle.eager import eager_msda  # noqa: PLC0415
 
-    cfg = CONFIGS[4]
-    sample_queries = 21504
+    cfg = CONFIGS[config]
+    queries = make_workload(cfg, batch=1).sizes[4]
+    sample_queries = min(queries, 21504)
     w = make_workload(cfg, batch=1, queries=sample_queries).to("cpu", dtype, loc_dtype)
     value, shapes, starts, loc, attn = w.operands(softmax=softmax)
     times = []
@@ -147,7 +155,7 @@ def cpu_baseline(dtype: torch.dtype, loc_dtype: torch.dtype, softmax: bool) -> d
         out.backward(w.grad_output)
         if i:
             times.append(time.perf_counter() - t0)
-    full_pairs = cfg.batch * 21504
+    full_pairs = cfg.batch * queries
     scale = full_pairs / (1 * sample_queries)
     return {
         "value": statistics.median(times) * 1e3 * scale,
@@ -157,7 +165,7 @@ def cpu_baseline(dtype: torch.dtype, loc_dtype: torch.dtype, softmax: bool) -> d
         "sample": (
             f"torch restatement of the reference eager backend (backends/eager/msda_pytorch.py) "
             f"fwd + autograd bwd, {str(dtype).split('.')[-1]}, batch 1 x {sample_queries} queries "
-            f"of config 4 (1/{scale:g} of a call), median of 3 after 1 warm-up, scaled x{scale:g}; "
+            f"of config {config} (1/{scale:g} of a call), median of 3 after 1 warm-up, scaled x{scale:g}; "
             f"host {os.cpu_count()} logical CPUs"
         ),
     }
@@ -171,6 +179,7 @@ def main() -> int:
     parser.add_argument("--dtype", choices=sorted(DTYPES), default="bf16")
     parser.add_argument("--loc-dtype", choices=sorted(DTYPES), default=None)
     parser.add_argument("--method", choices=["linear", "softmax"], default="linear")
+    parser.add_argument("--config", type=int, choices=sorted(CONFIGS), default=4)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument(
         "--copy-calibration", type=int, default=0, metavar="MIB",
@@ -204,7 +213,8 @@ def main() -> int:
             torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads and writes MIB MiB
         torch.cuda.synchronize()
         del src, dst
-    w = make_workload(4).to(device, dtype, loc_dtype)
+    cfg = CONFIGS[args.config]
+    w = make_workload(cfg).to(device, dtype, loc_dtype)
     B, S, H, D, Q, L, P = w.sizes
     es = torch.empty((), dtype=dtype).element_size()
     ls = torch.empty((), dtype=loc_dtype).element_size()
@@ -215,7 +225,9 @@ def main() -> int:
     bwd_gbs = bwd_bytes / (kernels["backward"] * 1e-3) / 1e9
     total_gbs = (fwd_bytes + bwd_bytes) / (ms_per_step * 1e-3) / 1e9
 
-    profiled = args.dtype == "bf16" and loc_dtype == torch.bfloat16 and not softmax
+    profiled = args.config == 4 and args.dtype == "bf16" and loc_dtype == torch.bfloat16 and not softmax
+    levels = "/".join(f"{h}x{w_}" for h, w_ in cfg.levels)
+    queries = f"Q=S={S}" if cfg.queries is None else f"Q={Q}, S={S}"
     line = {
         "metric": METRIC,
         "value": round(ms_per_step, 5),
@@ -231,7 +243,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": (
-                f"config 4 m2f-large: B={B}, levels 128x128/64x64/32x32, Q=S={S}, H={H}, D={D}, "
+                f"config {args.config} {cfg.name}: B={B}, levels {levels}, {queries}, H={H}, D={D}, "
                 f"P={P}, {args.dtype} value/weights, {str(loc_dtype).split('.')[-1]} locations, "
                 f"{args.method} method, fwd+bwd via deformops_amd.registry.msda"
             ),
@@ -256,7 +268,7 @@ def main() -> int:
         },
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(dtype, loc_dtype, softmax)
+        line["cpu_baseline"] = cpu_baseline(args.config, dtype, loc_dtype, softmax)
     print(json.dumps(line), flush=True)
     return 0
 
