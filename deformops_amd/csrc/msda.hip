@@ -1837,22 +1837,40 @@ constexpr int kMfmaSubLog2 = 3;   // 8 x 8 position tiles of four 4 x 4 sub-tile
 constexpr int kMfmaK = 64;        // candidates per K-block: one per lane, two MFMA K-steps
 constexpr int kMfmaKStep = 32;    // the MFMA's K
 constexpr int kMfmaMaxNb = 4;     // 16-channel column blocks: D <= 64
-constexpr int kMfmaWBytes = 16 * kMfmaKStep * 2;  // one 16 x 32 weight tile
 
+// One 16 x 32 weight tile (16 positions, one K-step of candidates) in the value
+// dtype's width, and the LDS stride of a staged grad_out row. float rows get 16
+// bytes of padding: the fp32 MFMA's B operand reads four rows at once.
+constexpr int mfma_wbytes(int es) { return 16 * kMfmaKStep * es; }
+constexpr int mfma_row_stride(int nb, int es) { return 16 * nb * es + (es == 4 ? 16 : 0); }
+
+// The MFMA of each value dtype. 16-bit values: v_mfma_f32_16x16x32_{bf16,f16}, the
+// weight rounded to the value dtype (W). float: v_mfma_f32_16x16x4_f32, eight per
+// K-step, the weight exact.
 template <typename T> struct MfmaOp;
 template <> struct MfmaOp<bf16_t> {
   using V = bf16x8_v;
+  using W = uint16_t;
   static __device__ inline f32x4_v mma(V a, V b, f32x4_v c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
-  static __device__ inline uint16_t round(float w) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(w)); }
+  static __device__ inline W round(float w) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(w)); }
 };
 template <> struct MfmaOp<f16_t> {
   using V = f16x8_v;
+  using W = uint16_t;
   static __device__ inline f32x4_v mma(V a, V b, f32x4_v c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
-  static __device__ inline uint16_t round(float w) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(w)); }
+  static __device__ inline W round(float w) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(w)); }
+};
+template <> struct MfmaOp<float> {
+  using V = float;
+  using W = uint32_t;
+  static __device__ inline f32x4_v mma(V a, V b, f32x4_v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+  static __device__ inline W round(float w) { return __builtin_bit_cast(uint32_t, w); }
 };
 
 // A wave-uniform value moved to a scalar register (it is the same in every lane).
@@ -1871,8 +1889,9 @@ __device__ inline i16x4_v lds_read_tr16(const unsigned char* p) {
 
 // Per-wave LDS of the matrix-core kernel: the staged rows and the four weight
 // tiles during a tile, the wave's partial sums at its end.
-size_t mfma_wave_bytes(int64_t D) {
-  const size_t work = size_t(kMfmaK) * size_t(2 * D) + 4 * size_t(kMfmaWBytes);  // rows + 4 weight tiles
+size_t mfma_wave_bytes(int64_t D, int es) {
+  const size_t work = size_t(kMfmaK) * size_t(mfma_row_stride(int(D / 16), es)) +
+                      4 * size_t(mfma_wbytes(es));  // rows + 4 weight tiles
   const size_t partial = 4 * size_t(D / 16) * kWave * 16;
   return std::max(work, partial);
 }
@@ -1883,7 +1902,9 @@ size_t mfma_head_bytes(int64_t L) {
   return at + 16;
 }
 
-size_t mfma_lds_bytes(int64_t L, int64_t D) { return mfma_head_bytes(L) + kMfmaWaves * mfma_wave_bytes(D); }
+size_t mfma_lds_bytes(int64_t L, int64_t D, int es) {
+  return mfma_head_bytes(L) + kMfmaWaves * mfma_wave_bytes(D, es);
+}
 
 // The candidates of one tile: ranges of the entry list (the tile's own
 // sub-buckets, then its neighbours' straddlers); candidate c sits at entry
@@ -1947,9 +1968,11 @@ template <typename T, typename TL> struct MfmaMeta {
   T attn;              // the weight, or with softmax the logit
   SoftStat<float> st;  // softmax: the unit's statistics (when stats are kept)
 };
-template <int NB> struct MfmaRows {
-  u32x4_v piece[2 * NB];
+template <int NP> struct MfmaRows {
+  u32x4_v piece[NP];
 };
+// 16-byte pieces of one grad_out row of 16 NB channels (each lane loads as many).
+template <typename T, int NB> constexpr int mfma_pieces() { return NB * int(sizeof(T)); }
 
 // Per-tile constants of the matrix-core kernel (all wave-uniform).
 struct MfmaTile {
@@ -1969,17 +1992,17 @@ template <typename T, typename TL, bool SOFTMAX>
 __device__ inline void mfma_load_meta(const MfmaTile& t, uint32_t e, MfmaMeta<T, TL>& d) {
   const uint32_t q = fdiv(e, t.div_lp), s = e - q * uint32_t(t.LP);
   d.loc = *reinterpret_cast<const LocPair<TL>*>(t.loc + (__umul24(q, t.loc_q) + s * uint32_t(2 * sizeof(TL))));
-  if (!SOFTMAX || t.stats) d.attn = *reinterpret_cast<const T*>(t.attn + (__umul24(q, t.attn_q) + s * 2u));
+  if (!SOFTMAX || t.stats) d.attn = *reinterpret_cast<const T*>(t.attn + (__umul24(q, t.attn_q) + s * uint32_t(sizeof(T))));
   if constexpr (SOFTMAX)
     if (t.stats) d.st = t.stats[__umul24(q, uint32_t(t.H))];
 }
 
-template <int NB>
-__device__ inline void mfma_load_rows(const MfmaTile& t, uint32_t e, int lane, MfmaRows<NB>& d) {
-  constexpr int kPieces = NB * 2;  // 16-byte pieces per grad_out row (2 * 16 NB bytes)
+template <typename T, int NB>
+__device__ inline void mfma_load_rows(const MfmaTile& t, uint32_t e, int lane, MfmaRows<mfma_pieces<T, NB>()>& d) {
+  constexpr int kPieces = mfma_pieces<T, NB>();  // 16-byte pieces per grad_out row
   const uint32_t q = fdiv(e, t.div_lp);
 #pragma unroll
-  for (int j = 0; j < 2 * NB; ++j) {
+  for (int j = 0; j < kPieces; ++j) {
     const int f = lane + kWave * j, row = f / kPieces, pc = f - row * kPieces;
     const uint32_t qr = uint32_t(__shfl(int(q), row));
     d.piece[j] = *reinterpret_cast<const u32x4_v*>(t.gout + (__umul24(qr, t.gout_q) + uint32_t(pc * 16)));
@@ -1992,20 +2015,24 @@ __device__ inline void mfma_load_rows(const MfmaTile& t, uint32_t e, int lane, M
 // LDS, after which the row registers are free for the next block's loads. Part B:
 // per MFMA K-step (the candidates of lanes 0-31, then 32-63) scatter the corner
 // weights into the zeroed weight tiles and run the four sub-tiles' MFMAs.
-struct MfmaCorners {
+template <typename W> struct MfmaCorners {
   int o[4];
-  uint16_t w[4];
+  W w[4];
 };
 
 template <typename T, typename TL, int NB, bool SOFTMAX>
-__device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, uint32_t kb, uint32_t e,
-                                           const MfmaMeta<T, TL>& d, const MfmaRows<NB>& rows, int lane,
-                                           unsigned char* gst) {
+__device__ inline MfmaCorners<typename MfmaOp<T>::W> mfma_kblock_a(const MfmaTile& t, const Level& lv, uint32_t kb,
+                                                                  uint32_t e, const MfmaMeta<T, TL>& d,
+                                                                  const MfmaRows<mfma_pieces<T, NB>()>& rows,
+                                                                  int lane, unsigned char* gst) {
   using Op = MfmaOp<T>;
-  constexpr int kPieces = NB * 2;
+  constexpr int ES = int(sizeof(T));
+  constexpr int kPieces = mfma_pieces<T, NB>();
+  constexpr int kRowStride = mfma_row_stride(NB, ES);
+  constexpr int kWBytes = mfma_wbytes(ES);
   const int kc = lane & (kMfmaKStep - 1);
   const uint32_t c = kb * kMfmaK + uint32_t(lane);
-  MfmaCorners cr;
+  MfmaCorners<typename Op::W> cr;
   float w[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int k = 0; k < 4; ++k) cr.o[k] = -1;
@@ -2028,9 +2055,12 @@ __device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, 
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int y = y0 + (k >> 1), x = x0 + (k & 1);
-      // Position (y, x) of the tile: sub-tile (y / 4) * 2 + x / 4, row (y % 4) * 4 + x % 4.
+      // Position (y, x) of the tile: sub-tile (y / 4) * 2 + x / 4, row (y % 4) * 4 + x % 4
+      // of its weight tile, which is position-major for 16-bit values ([16][32]) and
+      // candidate-major for float ([32][16]), the layouts the MFMAs read.
       if (m[k] && y >= 0 && x >= 0 && t.r0 + y < t.r1 && t.c0 + x < t.c1) {
-        cr.o[k] = ((y >> 2) * 2 + (x >> 2)) * kMfmaWBytes + ((y & 3) * 4 + (x & 3)) * (2 * kMfmaKStep) + kc * 2;
+        const int pos = (y & 3) * 4 + (x & 3);
+        cr.o[k] = ((y >> 2) * 2 + (x >> 2)) * kWBytes + (ES == 4 ? (kc * 16 + pos) * 4 : pos * (2 * kMfmaKStep) + kc * 2);
         w[k] = wb[k] * a;
       }
     }
@@ -2040,20 +2070,23 @@ __device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, 
   wave_lds_order();  // after the previous K-block's operand reads
   const u32x4_v zero = {0u, 0u, 0u, 0u};
 #pragma unroll
-  for (int j = 0; j < 2 * NB; ++j) {
-    const int f = lane + kWave * j, row = f / kPieces;
+  for (int j = 0; j < kPieces; ++j) {
+    const int f = lane + kWave * j, row = f / kPieces, pc = f - row * kPieces;
     const bool ok = kb * kMfmaK + uint32_t(row) < t.ncand;  // past the end: zero rows
-    *reinterpret_cast<u32x4_v*>(gst + f * 16) = ok ? rows.piece[j] : zero;
+    *reinterpret_cast<u32x4_v*>(gst + row * kRowStride + pc * 16) = ok ? rows.piece[j] : zero;
   }
   return cr;
 }
 
 template <typename T, int NB>
-__device__ inline void mfma_kblock_b(const MfmaCorners& cr, int lane, const unsigned char* gst,
+__device__ inline void mfma_kblock_b(const MfmaCorners<typename MfmaOp<T>::W>& cr, int lane, const unsigned char* gst,
                                      unsigned char* wt, f32x4_v (&acc)[4][NB]) {
   using Op = MfmaOp<T>;
   using V = typename Op::V;
-  constexpr int kRowBytes = 32 * NB;
+  using W = typename Op::W;
+  constexpr int ES = int(sizeof(T));
+  constexpr int kRowBytes = mfma_row_stride(NB, ES);
+  constexpr int kWBytes = mfma_wbytes(ES);
   const int half = lane >> 5;
   const int g16 = lane >> 4, i16 = lane & 15;
   const u32x4_v zero = {0u, 0u, 0u, 0u};
@@ -2061,29 +2094,50 @@ __device__ inline void mfma_kblock_b(const MfmaCorners& cr, int lane, const unsi
   for (int ks = 0; ks < 2; ++ks) {
     wave_lds_order();
 #pragma unroll
-    for (int st = 0; st < 4; ++st) *reinterpret_cast<u32x4_v*>(wt + st * kMfmaWBytes + lane * 16) = zero;
+    for (int z = 0; z < 4 * kWBytes / (kWave * 16); ++z)
+      *reinterpret_cast<u32x4_v*>(wt + (z * kWave + lane) * 16) = zero;
     wave_lds_order();
     if (half == ks) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        if (cr.o[k] >= 0) *reinterpret_cast<uint16_t*>(wt + cr.o[k]) = cr.w[k];
+        if (cr.o[k] >= 0) *reinterpret_cast<W*>(wt + cr.o[k]) = cr.w[k];
     }
     wave_lds_order();
-    V bv[NB];
+    if constexpr (ES == 4) {
+      // v_mfma_f32_16x16x4_f32, lane l (g = l / 16, i = l % 16): A[i][g] = the weight of
+      // candidate 4 kk + g at position i (candidate-major tiles: conflict-free reads),
+      // B[g][i] = channel 16 nb + i of that candidate's grad_out row; C as above.
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const unsigned char* src =
-          gst + (kMfmaKStep * ks + 8 * g16 + i16 / 4) * kRowBytes + (16 * nb + 4 * (i16 & 3)) * 2;
-      const i16x4_v t0 = lds_read_tr16(src);
-      const i16x4_v t1 = lds_read_tr16(src + 4 * kRowBytes);
-      bv[nb] = __builtin_bit_cast(V, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7));
-    }
-    const int aoff = i16 * (2 * kMfmaKStep) + g16 * 16;
+      for (int kk = 0; kk < kMfmaKStep / 4; ++kk) {
+        const int row = kMfmaKStep * ks + 4 * kk + g16;
+        float bv[NB];
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const V av = __builtin_bit_cast(V, *reinterpret_cast<const u32x4_v*>(wt + st * kMfmaWBytes + aoff));
+        for (int nb = 0; nb < NB; ++nb)
+          bv[nb] = *reinterpret_cast<const float*>(gst + row * kRowBytes + (16 * nb + i16) * 4);
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[st][nb] = Op::mma(av, bv[nb], acc[st][nb]);
+        for (int st = 0; st < 4; ++st) {
+          const float av = *reinterpret_cast<const float*>(wt + st * kWBytes + ((4 * kk + g16) * 16 + i16) * 4);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) acc[st][nb] = Op::mma(av, bv[nb], acc[st][nb]);
+        }
+      }
+    } else {
+      V bv[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const unsigned char* src =
+            gst + (kMfmaKStep * ks + 8 * g16 + i16 / 4) * kRowBytes + (16 * nb + 4 * (i16 & 3)) * 2;
+        const i16x4_v t0 = lds_read_tr16(src);
+        const i16x4_v t1 = lds_read_tr16(src + 4 * kRowBytes);
+        bv[nb] = __builtin_bit_cast(V, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7));
+      }
+      const int aoff = i16 * (2 * kMfmaKStep) + g16 * 16;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const V av = __builtin_bit_cast(V, *reinterpret_cast<const u32x4_v*>(wt + st * kWBytes + aoff));
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[st][nb] = Op::mma(av, bv[nb], acc[st][nb]);
+      }
     }
   }
 }
@@ -2108,25 +2162,25 @@ __device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, con
   const uint32_t step = uint32_t(kbstep) * kMfmaK;
   uint32_t cand = uint32_t(kb0) * kMfmaK + uint32_t(lane);  // this lane's candidate in block j
   MfmaMeta<T, TL> ma, mb;
-  MfmaRows<NB> rows;
+  MfmaRows<mfma_pieces<T, NB>()> rows;
   uint32_t ea = 0, eb = 0, j = 0;
   if (mine > 0) {
     ea = cand_entry(ent, cr, cand);
     eb = cand_entry(ent, cr, cand + step);
     mfma_load_meta<T, TL, SOFTMAX>(t, ea, ma);
-    mfma_load_rows<NB>(t, ea, lane, rows);
+    mfma_load_rows<T, NB>(t, ea, lane, rows);
   }
   for (; j + 2 < mine; j += 2) {
     const uint32_t kb = uint32_t(kb0) + j * uint32_t(kbstep);
     const uint32_t e2 = cand_entry(ent, cr, cand + 2 * step);
     mfma_load_meta<T, TL, SOFTMAX>(t, eb, mb);
-    MfmaCorners c0 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ma, rows, lane, gst);
-    mfma_load_rows<NB>(t, eb, lane, rows);
+    const auto c0 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ma, rows, lane, gst);
+    mfma_load_rows<T, NB>(t, eb, lane, rows);
     mfma_kblock_b<T, NB>(c0, lane, gst, wt, acc);
     const uint32_t e3 = cand_entry(ent, cr, cand + 3 * step);
     mfma_load_meta<T, TL, SOFTMAX>(t, e2, ma);
-    MfmaCorners c1 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, mb, rows, lane, gst);
-    mfma_load_rows<NB>(t, e2, lane, rows);
+    const auto c1 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, mb, rows, lane, gst);
+    mfma_load_rows<T, NB>(t, e2, lane, rows);
     mfma_kblock_b<T, NB>(c1, lane, gst, wt, acc);
     ea = e2;
     eb = e3;
@@ -2136,11 +2190,11 @@ __device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, con
     const uint32_t kb = uint32_t(kb0) + j * uint32_t(kbstep);
     const bool two = j + 1 < mine;
     if (two) mfma_load_meta<T, TL, SOFTMAX>(t, eb, mb);
-    MfmaCorners c0 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ma, rows, lane, gst);
-    if (two) mfma_load_rows<NB>(t, eb, lane, rows);
+    const auto c0 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ma, rows, lane, gst);
+    if (two) mfma_load_rows<T, NB>(t, eb, lane, rows);
     mfma_kblock_b<T, NB>(c0, lane, gst, wt, acc);
     if (two) {
-      MfmaCorners c1 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, mb, rows, lane, gst);
+      const auto c1 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, mb, rows, lane, gst);
       mfma_kblock_b<T, NB>(c1, lane, gst, wt, acc);
     }
   }
@@ -2222,7 +2276,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
     const Problem p, const BwdGeom bg, int* __restrict__ buckets,
     const uint32_t* __restrict__ entries, const int accumulate) {
   constexpr int D = 16 * NB;
-  constexpr int ES = 2;
+  constexpr int ES = int(sizeof(T));
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ int table[kMfmaTable + 1];  // per (pair, level): prefix count of chunks
   __shared__ int ntab[kMfmaTable];       // per (pair, level): tasks
@@ -2245,11 +2299,11 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
   at = (at + 15) & ~size_t(15);
   int64_t* total = reinterpret_cast<int64_t*>(smem + at);  // [0]: tiles, [1]: the fetched task
   at += 16;
-  constexpr size_t kWaveBytes = std::max(size_t(kMfmaK * 32 * NB) + 4 * size_t(kMfmaWBytes),
-                                         size_t(4 * NB * kWave * 16));
+  constexpr size_t kRowsBytes = size_t(kMfmaK) * size_t(mfma_row_stride(NB, ES));
+  constexpr size_t kWaveBytes = std::max(kRowsBytes + 4 * size_t(mfma_wbytes(ES)), size_t(4 * NB * kWave * 16));
   unsigned char* region0 = smem + at;
   unsigned char* gst = region0 + size_t(wave) * kWaveBytes;  // grad_out rows
-  unsigned char* wt = gst + kMfmaK * 32 * NB;                // four weight tiles
+  unsigned char* wt = gst + kRowsBytes;                      // four weight tiles
 
   const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
   if (!accumulate) {
@@ -2871,15 +2925,16 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   const int64_t attn_bytes = B * samples_bh * H * es;
   const bool attn_ok = (reinterpret_cast<uintptr_t>(grad_attn) & 3) == 0;
   bg.keys_alloc = attn_ok && samples_bh < (int64_t(1) << 32) ? attn_bytes / (4 * B * H) : 0;
-  // The matrix-core grad_value: 16-bit dtypes, D in {16, 32, 48, 64} with 16-byte
+  // The matrix-core grad_value: float and 16-bit dtypes, D in {16, 32, 48, 64} with 16-byte
   // aligned rows, and bucket counters for 4 x 4 tiles surely in the scratch. A level
   // of h x w positions has ceil(h / 4) ceil(w / 4) <= h w / 4 + 1 such tiles.
   // A level of h x w positions has ceil(h / 8) ceil(w / 8) <= h w / 8 + 1 8 x 8 tiles.
   const int64_t mfma_tiles_bound = L * (S / 8 + 1);
   const int64_t ls = elem_size(loc_dtype);
   const int64_t per_image = Q * H * std::max(L * P * 2 * ls, D * es);  // 32-bit offsets inside an image
-  bool mfma_ok = (dtype == MSDA_BF16 || dtype == MSDA_F16) && D % 16 == 0 && D / 16 <= kMfmaMaxNb &&
-                 4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc && mfma_lds_bytes(L, D) <= lds_limit &&
+  bool mfma_ok = (dtype == MSDA_BF16 || dtype == MSDA_F16 || dtype == MSDA_F32) && D % 16 == 0 &&
+                 D / 16 <= kMfmaMaxNb && 4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc &&
+                 mfma_lds_bytes(L, D, int(es)) <= lds_limit &&
                  B * H * mfma_tiles_bound < (int64_t(1) << 31) && per_image < (int64_t(1) << 31) &&
                  getenv("DEFORMOPS_AMD_NO_MFMA") == nullptr;
   for (int i = 0; i < n_chan && mfma_ok; ++i) mfma_ok = aligned(vec_ptrs[i], 16);
@@ -2904,7 +2959,7 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   plan->owner_blocks = xcd_group_grid(H, int64_t(bg.nw) * B);
   plan->owner_lds = owner_lds_bytes(dtype, L, D, bg.nb, bg.cap);
   plan->mfma_nb = int(D / 16);
-  plan->mfma_lds = mfma_lds_bytes(L, D);
+  plan->mfma_lds = mfma_lds_bytes(L, D, int(es));
   if (mfma_ok) {
     // Persistent workgroups, as many as fit the CUs at once, a multiple of 8.
     const int64_t static_lds = sizeof(int) * (2 * kMfmaTable + 1 + kMfmaWaves + 2);
@@ -2980,7 +3035,7 @@ hipError_t launch_owner_cvr(const BackwardPlan& plan, const Problem& p, const in
 template <typename T, typename TL, bool SM>
 hipError_t launch_owner_mfma(const BackwardPlan& plan, const Problem& p, const int* buckets,
                              const uint32_t* entries, int accumulate, hipStream_t st) {
-  if constexpr (std::is_same_v<T, bf16_t> || std::is_same_v<T, f16_t>) {
+  if constexpr (std::is_same_v<T, bf16_t> || std::is_same_v<T, f16_t> || std::is_same_v<T, float>) {
     auto go = [&](auto k) -> hipError_t {
       const hipError_t e = allow_lds(k, plan.mfma_lds);
       if (e != hipSuccess) return e;

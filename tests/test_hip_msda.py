@@ -165,15 +165,16 @@ def test_wider_shapes_at_encoder_size(device, sizes, dtype):
                              label=f"config 2 with {sizes}")
 
 
-# The two grad_value kernels for 16-bit dtypes: the matrix-core one (the default for
-# D = 16, 32, 48, 64) and the VALU owner kernel (every other case, and the fallback
-# when the bucket scratch is short), selected by DEFORMOPS_AMD_NO_MFMA; and the two
+# The two grad_value kernels for float and 16-bit dtypes: the matrix-core one (the
+# default for D = 16, 32, 48, 64) and the VALU owner kernel (every other case, float64,
+# and the fallback when the bucket scratch is short), selected by
+# DEFORMOPS_AMD_NO_MFMA; and the two
 # ways the bucket sort publishes its counts: per-workgroup count rows (the default
 # where the scratch has room) or global atomics, forced by DEFORMOPS_AMD_ATOMIC_SORT.
 
 
 @pytest.mark.parametrize("path", ["mfma", "mfma-atomic-sort", "valu", "valu-atomic-sort"])
-@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("dtype", [BF16, F16, F32], ids=["bf16", "f16", "f32"])
 @pytest.mark.parametrize("cfg", [2, 3])
 def test_grad_value_paths_match_oracle(device, monkeypatch, cfg, dtype, path):
     if path.startswith("valu"):
