@@ -44,7 +44,7 @@ PEAK_HBM_GBS = 8000.0
 # and locations, linear method): rocprofv3 FETCH_SIZE x 2 + WRITE_SIZE x 1, summed
 # over the call's kernels, each counter scaled by what it reads for a 256 MiB copy.
 # profiles/msda_config4_bf16_hbm_traffic.md holds the passes and the calibration.
-BACKWARD_TRAFFIC_BYTES = 1_133_424_727
+BACKWARD_TRAFFIC_BYTES = 1_129_519_424
 DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 
 
