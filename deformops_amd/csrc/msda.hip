@@ -894,6 +894,16 @@ __device__ inline bool chunked_sort(const Problem& p, const BwdGeom& bg, int64_t
   return need <= bh * bg.keys_alloc;
 }
 
+// Whether the bucket counters of every (b, h) and, after them, the matrix-core
+// kernel's work-queue counters fit the scratch. The host picks the matrix-core
+// kernel from an estimate of the tile count; the kernels that touch the queue
+// counters check the real count here, and the VALU owner kernel runs instead when
+// they do not fit.
+__device__ inline bool queue_fits(const Problem& p, const BwdGeom& bg, int64_t nkeys) {
+  const int64_t bh = int64_t(p.B) * p.H;
+  return nkeys <= bg.keys_alloc && bh * nkeys + kQueueInts <= bh * bg.keys_alloc;
+}
+
 // Per-unit softmax statistics for the grad_value kernels: the max and the sum of
 // exp(logit - max) of every (b, q, h), written by msda_softmax_stats_kernel after
 // the place pass (over the per-workgroup counts, done with by then), where the
@@ -1321,7 +1331,7 @@ __global__ __launch_bounds__(256) void msda_bucket_clear_kernel(const Problem p,
   if (ntiles < 0 || nkeys > bg.keys_alloc) return;
   if (chunked_sort(p, bg, nkeys)) return;  // the passes write every count; the scan clears the queues
   // The matrix-core grad_value keeps its work-queue counters right after the rows.
-  const int64_t n = int64_t(p.B) * p.H * nkeys + (bg.sub_log2 > 0 ? kQueueInts : 0);
+  const int64_t n = int64_t(p.B) * p.H * nkeys + (bg.sub_log2 > 0 && queue_fits(p, bg, nkeys) ? kQueueInts : 0);
   const int64_t stride = int64_t(gridDim.x) * blockDim.x;
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) buckets[i] = 0;
 }
@@ -1514,7 +1524,7 @@ __device__ inline void order_levels(const Problem& p, const Level* levels, const
 template <typename T, typename TL, int CVR, bool SOFTMAX>
 __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
     const Problem p, const BwdGeom bg, const int* __restrict__ buckets,
-    const uint32_t* __restrict__ entries, const int accumulate) {
+    const uint32_t* __restrict__ entries, const int accumulate, const int after_mfma) {
   using A = typename Elem<T>::acc;
   using PieceT = Piece<T, CVR>;
   constexpr int ES = Elem<T>::size;
@@ -1553,6 +1563,7 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
 
   const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
   if (ntiles <= 0) return;
+  if (after_mfma && queue_fits(p, bg, 4 * ntiles)) return;  // the matrix-core kernel did the work
   const bool bucketed = 4 * ntiles <= bg.keys_alloc;
   const SoftStat<A>* stats = SOFTMAX && bucketed && softmax_stats_fit<A>(p, bg, 4 * ntiles, buckets)
                                  ? softmax_stats<A>(const_cast<int*>(buckets), p, 4 * ntiles)
@@ -2323,7 +2334,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
       }
     }
   }
-  if (ntiles <= 0 || 4 * ntiles > bg.keys_alloc) return;  // the host launches this only when bucketed
+  if (ntiles <= 0 || !queue_fits(p, bg, 4 * ntiles)) return;  // the VALU owner kernel runs instead
   const bool stats_ok = SOFTMAX && softmax_stats_fit<float>(p, bg, 4 * ntiles, buckets);
   if (tid == 0) {
     order_levels(p, levels, lt, order, rank_base);
@@ -2852,7 +2863,10 @@ struct BackwardPlan {
   int64_t bucket_chunks;  // bucketing workgroups per (b, h)
   int64_t zero_keys;      // bucket counters to clear per (b, h), at most
   int64_t scan_blocks;    // workgroups of msda_bucket_scan_kernel
-  bool mfma;              // grad_value on the matrix cores (4 x 4 tiles)
+  bool mfma;              // grad_value on the matrix cores (8 x 8 tiles)
+  bool mfma_fallback;     // and the VALU owner kernel after it, for when its counters do not fit
+  int fallback_nw;        // that launch's persistent tile slots per (b, h): a small grid, since it
+  int64_t fallback_blocks;  // returns at once whenever the matrix-core kernel did the work
   int mfma_nb;            // 16-channel column blocks
   int64_t mfma_blocks;
   size_t mfma_lds;
@@ -2925,20 +2939,31 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   const int64_t attn_bytes = B * samples_bh * H * es;
   const bool attn_ok = (reinterpret_cast<uintptr_t>(grad_attn) & 3) == 0;
   bg.keys_alloc = attn_ok && samples_bh < (int64_t(1) << 32) ? attn_bytes / (4 * B * H) : 0;
-  // The matrix-core grad_value: float and 16-bit dtypes, D in {16, 32, 48, 64} with 16-byte
-  // aligned rows, and bucket counters for 4 x 4 tiles surely in the scratch. A level
-  // of h x w positions has ceil(h / 4) ceil(w / 4) <= h w / 4 + 1 such tiles.
-  // A level of h x w positions has ceil(h / 8) ceil(w / 8) <= h w / 8 + 1 8 x 8 tiles.
+  // The matrix-core grad_value: float and 16-bit dtypes, D in {16, 32, 48, 64} with
+  // 16-byte aligned rows, and its bucket and queue counters (4 per 8 x 8 tile) in the
+  // scratch. A level of h x w positions has ceil(h / 8) ceil(w / 8) <= h w / 8 + 1
+  // such tiles (the bound of a 1-row level). When that bound does not fit (few queries
+  // against a large pyramid, as in a decoder), an estimate for levels of aspect ratio
+  // at most 4 decides: ceil(h / 8) ceil(w / 8) <= h w / 64 + (h + w) / 8 + 1 with
+  // h + w <= 2.5 sqrt(h w), and sum_l sqrt(h_l w_l) <= sqrt(L S). The kernels then
+  // check the real count, and the VALU owner kernel (which takes 8 x 8 tiles when
+  // its capacity is at least 64 positions) runs after the matrix-core one and works
+  // only if the counters did not fit.
   const int64_t mfma_tiles_bound = L * (S / 8 + 1);
+  const int64_t mfma_tiles_estimate =
+      S / 64 + int64_t(ceil(2.5 * sqrt(double(L) * double(S)) / 8.0)) + 2 * L;
   const int64_t ls = elem_size(loc_dtype);
   const int64_t per_image = Q * H * std::max(L * P * 2 * ls, D * es);  // 32-bit offsets inside an image
+  const bool mfma_sure = 4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc;
+  const bool mfma_likely = 4 * mfma_tiles_estimate + kQueueInts <= bg.keys_alloc && bg.cap >= 64;
   bool mfma_ok = (dtype == MSDA_BF16 || dtype == MSDA_F16 || dtype == MSDA_F32) && D % 16 == 0 &&
-                 D / 16 <= kMfmaMaxNb && 4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc &&
+                 D / 16 <= kMfmaMaxNb && (mfma_sure || mfma_likely) &&
                  mfma_lds_bytes(L, D, int(es)) <= lds_limit &&
                  B * H * mfma_tiles_bound < (int64_t(1) << 31) && per_image < (int64_t(1) << 31) &&
                  getenv("DEFORMOPS_AMD_NO_MFMA") == nullptr;
   for (int i = 0; i < n_chan && mfma_ok; ++i) mfma_ok = aligned(vec_ptrs[i], 16);
   plan->mfma = mfma_ok;
+  plan->mfma_fallback = mfma_ok && !mfma_sure;
   bg.sub_log2 = mfma_ok ? kMfmaSubLog2 : 0;
   if (mfma_ok) bg.amin = 1 << (2 * kMfmaSubLog2);
   // Tiles per (b, h): every level has at most 3 h w / amin + 1 adaptive tiles.
@@ -2957,6 +2982,8 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   plan->bucket_lds = bucket_head + size_t(bg.keys_lds) * 4;
   plan->bucket_chunks = (samples_bh + kBucketThreads * kBucketSamples - 1) / (kBucketThreads * kBucketSamples);
   plan->owner_blocks = xcd_group_grid(H, int64_t(bg.nw) * B);
+  plan->fallback_nw = int(std::max<int64_t>(1, std::min<int64_t>(bg.nw, (2 * int64_t(cus) + B * H - 1) / (B * H))));
+  plan->fallback_blocks = xcd_group_grid(H, int64_t(plan->fallback_nw) * B);
   plan->owner_lds = owner_lds_bytes(dtype, L, D, bg.nb, bg.cap);
   plan->mfma_nb = int(D / 16);
   plan->mfma_lds = mfma_lds_bytes(L, D, int(es));
@@ -3006,27 +3033,35 @@ hipError_t allow_lds(Kernel k, size_t bytes) {
 
 template <typename T, typename TL, int CVR, bool SM>
 hipError_t launch_owner(const BackwardPlan& plan, const Problem& p, const int* buckets,
-                        const uint32_t* entries, int accumulate, hipStream_t st) {
+                        const uint32_t* entries, int accumulate, int after_mfma, hipStream_t st) {
   auto k = msda_grad_value_kernel<T, TL, CVR, SM>;
   const hipError_t e = allow_lds(k, plan.owner_lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k, dim3(unsigned(plan.owner_blocks)), dim3(kOwnerThreads), plan.owner_lds, st, p,
-                     plan.bg, buckets, entries, accumulate);
+  BwdGeom bg = plan.bg;
+  int64_t blocks = plan.owner_blocks;
+  if (after_mfma) {
+    bg.nw = plan.fallback_nw;
+    blocks = plan.fallback_blocks;
+  }
+  hipLaunchKernelGGL(k, dim3(unsigned(blocks)), dim3(kOwnerThreads), plan.owner_lds, st, p, bg, buckets, entries,
+                     accumulate, after_mfma);
   return hipGetLastError();
 }
 
 template <typename T, typename TL, bool SM>
 hipError_t launch_owner_cvr(const BackwardPlan& plan, const Problem& p, const int* buckets,
-                            const uint32_t* entries, int accumulate, hipStream_t st) {
+                            const uint32_t* entries, int accumulate, int after_mfma, hipStream_t st) {
   constexpr int kMaxCv = 16 / Elem<T>::size;
   switch (plan.cvr) {
-    case 1: return launch_owner<T, TL, 1, SM>(plan, p, buckets, entries, accumulate, st);
-    case 2: return launch_owner<T, TL, 2, SM>(plan, p, buckets, entries, accumulate, st);
+    case 1: return launch_owner<T, TL, 1, SM>(plan, p, buckets, entries, accumulate, after_mfma, st);
+    case 2: return launch_owner<T, TL, 2, SM>(plan, p, buckets, entries, accumulate, after_mfma, st);
     case 4:
-      if constexpr (kMaxCv >= 4) return launch_owner<T, TL, 4, SM>(plan, p, buckets, entries, accumulate, st);
+      if constexpr (kMaxCv >= 4)
+        return launch_owner<T, TL, 4, SM>(plan, p, buckets, entries, accumulate, after_mfma, st);
       break;
     case 8:
-      if constexpr (kMaxCv >= 8) return launch_owner<T, TL, 8, SM>(plan, p, buckets, entries, accumulate, st);
+      if constexpr (kMaxCv >= 8)
+        return launch_owner<T, TL, 8, SM>(plan, p, buckets, entries, accumulate, after_mfma, st);
       break;
   }
   return hipErrorInvalidValue;
@@ -3334,9 +3369,11 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
         if (plan.mfma)
           e = softmax ? launch_owner_mfma<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
                       : launch_owner_mfma<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
-        else
-          e = softmax ? launch_owner_cvr<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
-                      : launch_owner_cvr<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
+        if (e == hipSuccess && (!plan.mfma || plan.mfma_fallback)) {
+          const int after_mfma = plan.mfma ? 1 : 0;
+          e = softmax ? launch_owner_cvr<T, TL, true>(plan, p, buckets, entries, int(accumulate), after_mfma, st)
+                      : launch_owner_cvr<T, TL, false>(plan, p, buckets, entries, int(accumulate), after_mfma, st);
+        }
         if (e != hipSuccess) return e;
         const dim3 grid(unsigned(plan.sample.num_blocks)), block(unsigned(kWave * plan.sample.waves));
         if (softmax)

@@ -191,6 +191,20 @@ def test_grad_value_paths_match_oracle(device, monkeypatch, cfg, dtype, path):
                              label=f"config {cfg} {path}")
 
 
+@pytest.mark.parametrize(("dtype", "queries"), [(BF16, 256), (F32, 128)], ids=["bf16", "f32"])
+def test_counters_that_do_not_fit_fall_back_to_the_owner_kernel(device, dtype, queries):
+    """A 2 x 1024 level has 128 tiles of 8 x 8, where levels of aspect ratio up to 4
+    would have about 49. With these queries the weight-gradient scratch holds 512
+    counters per head: enough for the host's estimate, so the matrix-core kernel is
+    launched, but not for the real counters plus its queue counters, so it does
+    nothing and the VALU owner kernel launched after it computes grad_value."""
+    w = make_workload(0, levels=((2, 1024),), batch=1, queries=queries, heads=2, channels=32, points=4,
+                      seed=11).to(device, dtype)
+    for softmax in (False, True):
+        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                             label=f"2x1024 level, {queries} queries")
+
+
 @pytest.mark.parametrize("dtype", [BF16, F16, F32], ids=["bf16", "f16", "f32"])
 def test_samples_piled_on_one_tile(device, dtype):
     """Every sample of every query lands near one pixel: one tile owns them all, so a
