@@ -460,6 +460,11 @@ __device__ inline LaneMap map_lane(const Problem& p) {
   return m;
 }
 
+// Keeps the compiler from moving this wave's LDS accesses across it. The LDS
+// executes one wave's instructions in order, so lanes of a wave then see each
+// other's earlier writes without a barrier.
+__device__ inline void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
+
 // Copies bytes from global memory to LDS, `piece` bytes (16, 8, 4, 2 or 1, dividing
 // `bytes` and the alignment of both ends) per lane and step.
 __device__ inline void copy_pieces(unsigned char* dst, const char* src, int bytes, int piece, int lane) {
@@ -1336,7 +1341,11 @@ __global__ __launch_bounds__(256) void msda_bucket_clear_kernel(const Problem p,
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) buckets[i] = 0;
 }
 
-// The per-unit softmax statistics (see SoftStat), one thread per (b, q, h).
+// The per-unit softmax statistics (see SoftStat), one lane per (b, q, h). A wave's 64
+// units have contiguous logits: where they fit, the wave copies them to LDS with
+// wide coalesced loads first (one load per lane and 16 bytes instead of one per
+// logit at a 2- to 8-byte stride between lanes).
+constexpr int kStatBytes = 64;  // logit bytes per unit staged through LDS, at most
 template <typename T>
 __global__ __launch_bounds__(256) void msda_softmax_stats_kernel(const Problem p, const BwdGeom bg,
                                                                   int* __restrict__ buckets) {
@@ -1352,15 +1361,30 @@ __global__ __launch_bounds__(256) void msda_softmax_stats_kernel(const Problem p
   const int64_t nkeys = 4 * ntiles;
   if (ntiles < 0 || nkeys > bg.keys_alloc || !softmax_stats_fit<A>(p, bg, nkeys, buckets)) return;
   SoftStat<A>* st = softmax_stats<A>(buckets, p, nkeys);
+  __shared__ __align__(16) unsigned char lg_s[256 / kWave][kWave * kStatBytes];
   const int LP = p.L * p.P;
+  const int ub = LP * int(sizeof(T));
+  const bool staged = ub <= kStatBytes;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const int64_t units = int64_t(p.B) * p.Q * p.H;
-  for (int64_t u = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; u < units; u += int64_t(gridDim.x) * blockDim.x) {
+  const int64_t wave_step = int64_t(gridDim.x) * (blockDim.x / kWave) * kWave;
+  for (int64_t u0 = (int64_t(blockIdx.x) * (blockDim.x / kWave) + wave) * kWave; u0 < units; u0 += wave_step) {
+    const int64_t u = u0 + lane;
     const T* lg = reinterpret_cast<const T*>(p.attn) + u * LP;
-    A mx = -INFINITY;
-    for (int i = 0; i < LP; ++i) mx = fmax(mx, load_acc(lg + i));
-    A sum(0);
-    for (int i = 0; i < LP; ++i) sum += exp_acc(load_acc(lg + i) - mx);
-    st[u] = SoftStat<A>{mx, sum};
+    if (staged) {
+      const int n = int(min<int64_t>(kWave, units - u0));
+      copy_pieces(lg_s[wave], p.attn + u0 * ub, n * ub, p.attn_piece, lane);
+      wave_lds_order();
+      lg = reinterpret_cast<const T*>(lg_s[wave] + lane * ub);
+    }
+    if (u < units) {
+      A mx = -INFINITY;
+      for (int i = 0; i < LP; ++i) mx = fmax(mx, load_acc(lg + i));
+      A sum(0);
+      for (int i = 0; i < LP; ++i) sum += exp_acc(load_acc(lg + i) - mx);
+      st[u] = SoftStat<A>{mx, sum};
+    }
+    wave_lds_order();  // the lanes' reads come before the next copy
   }
 }
 
@@ -1887,11 +1911,6 @@ template <> struct MfmaOp<float> {
 // A wave-uniform value moved to a scalar register (it is the same in every lane).
 __device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ inline uint32_t uni(uint32_t v) { return uint32_t(__builtin_amdgcn_readfirstlane(int(v))); }
-
-// Keeps the compiler from moving this wave's LDS accesses across it. The LDS
-// executes one wave's instructions in order, so lanes of a wave then see each
-// other's earlier writes without a barrier.
-__device__ inline void wave_lds_order() { __asm__ volatile("" ::: "memory"); }
 
 __device__ inline i16x4_v lds_read_tr16(const unsigned char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
