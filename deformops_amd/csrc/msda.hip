@@ -909,13 +909,13 @@ __device__ inline bool queue_fits(const Problem& p, const BwdGeom& bg, int64_t n
   return nkeys <= bg.keys_alloc && bh * nkeys + kQueueInts <= bh * bg.keys_alloc;
 }
 
-// Per-unit softmax statistics for the grad_value kernels: the max and the sum of
-// exp(logit - max) of every (b, q, h), written by msda_softmax_stats_kernel after
+// Per-unit softmax statistics for the grad_value kernels: lse = max + log(sum of
+// exp(logit - max)) of every (b, q, h), written by msda_softmax_stats_kernel after
 // the place pass (over the per-workgroup counts, done with by then), where the
-// scratch has room. A candidate's weight is then exp(logit - max) / sum: one logit
-// and one statistics load instead of a pass over the unit's L * P logits.
+// scratch has room. A candidate's weight is then exp(logit - lse): one logit and one
+// 4-byte statistics load instead of a pass over the unit's L * P logits.
 template <typename A> struct SoftStat {
-  A mx, sum;
+  A lse;
 };
 template <typename A>
 __device__ inline SoftStat<A>* softmax_stats(int* buckets, const Problem& p, int64_t nkeys) {
@@ -1382,7 +1382,7 @@ __global__ __launch_bounds__(256) void msda_softmax_stats_kernel(const Problem p
       for (int i = 0; i < LP; ++i) mx = fmax(mx, load_acc(lg + i));
       A sum(0);
       for (int i = 0; i < LP; ++i) sum += exp_acc(load_acc(lg + i) - mx);
-      st[u] = SoftStat<A>{mx, sum};
+      st[u] = SoftStat<A>{mx + log(sum)};
     }
     wave_lds_order();  // the lanes' reads come before the next copy
   }
@@ -1747,7 +1747,7 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
           const int64_t u = unit0 + int64_t(q) * p.H;
           if (stats) {
             const SoftStat<A> st = stats[u];
-            a = exp_acc(load_acc(attn_all + u * LP + s) - st.mx) / st.sum;
+            a = exp_acc(load_acc(attn_all + u * LP + s) - st.lse);
           } else {
             a = unit_weight<T, true>(attn_all + u * LP, LP, int(s));
           }
@@ -2071,7 +2071,7 @@ __device__ inline MfmaCorners<typename MfmaOp<T>::W> mfma_kblock_a(const MfmaTil
     float a;
     if constexpr (SOFTMAX) {
       if (t.stats) {
-        a = exp_acc(to_acc(d.attn) - d.st.mx) / d.st.sum;
+        a = exp_acc(to_acc(d.attn) - d.st.lse);
       } else {
         const uint32_t q = fdiv(e, t.div_lp), s = e - q * uint32_t(t.LP);
         a = unit_weight<T, true>(reinterpret_cast<const T*>(t.attn + __umul24(q, t.attn_q)), t.LP, int(s));
