@@ -660,8 +660,13 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
 //                              indices in grad_sampling_locations, both overwritten
 //                              later by msda_grad_sample_kernel, so the backward
 //                              needs no memory beyond its outputs.
-//   msda_gap_zero_kernel       Zeroes grad_value at positions no valid level covers.
-//   msda_grad_value_kernel     One tile per workgroup (loop): reads the buckets that
+//   msda_softmax_stats_kernel  Softmax only: every (b, q, h)'s log-sum-exp.
+//   msda_grad_value_mfma_kernel  The owners on the matrix cores (described below,
+//                              with the choice between the two owner kernels); also
+//                              zeroes grad_value at positions no valid level covers.
+//   msda_gap_zero_kernel       That zeroing, for the VALU owner kernel.
+//   msda_grad_value_kernel     The VALU owners (float64, other D, and the fallback):
+//                              one tile per workgroup (loop): reads the buckets that
 //                              can reach the tile, stages their grad_out rows in
 //                              LDS, sorts their corner records by position (LDS
 //                              integer counting sort) and accumulates
@@ -1830,26 +1835,30 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// grad_value on the matrix cores: 16-bit value dtypes, D = 16, 32, 48 or 64.
+// grad_value on the matrix cores: bf16, f16 and float values, D = 16, 32, 48 or 64.
 //
 // Tiles are 8 x 8 positions (sub_log2 = 3), bucketed as above, each made of four
-// 4 x 4 sub-tiles. One workgroup owns one tile of one (b, h) at a time; its four
-// waves take the tile's K-blocks of 32 candidate samples round-robin and keep
-// partial sums of all four sub-tiles (16 positions x D channels each) in the fp32
-// accumulators of v_mfma_f32_16x16x32_{bf16,f16}:
+// 4 x 4 sub-tiles. A (tile, head) task keeps the partial sums of its four sub-tiles
+// (16 positions x D channels each) in the fp32 accumulators of the MFMA:
 //   C_st[m, n] += sum_k W_st[m, k] * G[k, n]
 // where G[k, :] is candidate k's grad_out row and W_st[m, k] the attention *
 // bilinear weight of its corner at position m of sub-tile st (zero where it has
-// none, so a sample adds exactly its corners in the tile). Per K-block a wave
-// stages the 32 grad_out rows in its own LDS (row-major, 2 D bytes per row),
-// scatters the candidates' corner weights into four zeroed 16 x 32 weight tiles,
-// and reads the operands back: A (weights) with ds_read_b128, B (grad_out,
-// K-major) with two ds_read_b64_tr_b16 per 16 channels. Two lanes serve one
-// candidate, each one row of its 2 x 2 footprint. The weight enters the MFMA
-// rounded to 16 bits (nearest even); products and sums are fp32. Waves do not wait
-// for each other inside a tile; the loads of the next K-block (and the entries of
-// the one after) are in flight while a K-block computes. At the end of the tile the
-// four partial sums meet in LDS and wave w writes sub-tile w.
+// none, so a sample adds exactly its corners in the tile). The candidates come in
+// K-blocks of 64, one per lane; light tasks run one per wave, heavy ones split their
+// K-blocks over the workgroup's four waves. Per K-block a wave stages the 64
+// grad_out rows in its own LDS (row-major), and per K-step of 32 candidates scatters
+// their corner weights into four zeroed weight tiles and reads the operands back.
+//   - bf16 / f16: v_mfma_f32_16x16x32_{bf16,f16}, one per sub-tile and 16 channels and
+//     K-step; A (position-major weight tiles) with ds_read_b128, B (grad_out, K-major)
+//     with two ds_read_b64_tr_b16 per 16 channels. The weight enters the MFMA rounded
+//     to 16 bits (nearest even).
+//   - float: v_mfma_f32_16x16x4_f32, eight per sub-tile and 16 channels and K-step;
+//     candidate-major weight tiles and rows padded by 16 bytes, read with ds_read_b32.
+//     The weight enters exact.
+// Products and sums are fp32. Waves do not wait for each other inside a task; the
+// loads of the next K-block (and the entries of the one after) are in flight while a
+// K-block computes. A split task's four partial sums meet in LDS at its end and wave
+// w writes sub-tile w.
 //
 // Operand layouts of v_mfma_f32_16x16x32 (wave64; lane l, g = l / 16, i = l % 16):
 //   A: halves A[i][8 g .. 8 g + 7];  B: halves B[8 g .. 8 g + 7][i];
