@@ -1,0 +1,74 @@
+"""Property-based parity of the HIP kernels with the CPU oracle over random shapes.
+
+The GPU counterpart of the reference's hypothesis parity test
+(``tests/deformops/test_msda_reference.py:31-88``), widened: batch, heads, head
+width, levels and their shapes, points, queries, value dtype and softmax / linear
+method are drawn together, and every example checks the forward and all three
+gradients against the float64 C oracle with the tolerances of
+``tests/test_hip_msda.py``. The owner kernel for grad_value (matrix cores or VALU)
+and the bucket sort's counting mode (per-workgroup rows or atomics) are drawn too,
+through the library's environment switches. Examples are derandomized, so a GPU run
+replays the same cases.
+"""
+
+from __future__ import annotations
+
+import os
+
+import pytest
+import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
+
+from tests.test_hip_msda import BF16, F16, F32, check_against_oracle
+from tests.workloads import make_workload
+
+pytestmark = pytest.mark.gpu
+
+PATHS = {
+    "default": {},
+    "valu": {"DEFORMOPS_AMD_NO_MFMA": "1"},
+    "atomic-sort": {"DEFORMOPS_AMD_ATOMIC_SORT": "1"},
+}
+
+
+@st.composite
+def cases(draw):
+    L = draw(st.integers(1, 5))
+    levels = tuple((draw(st.integers(1, 40)), draw(st.integers(1, 40))) for _ in range(L))
+    H = draw(st.sampled_from([1, 2, 3, 4, 8]))
+    D = draw(st.sampled_from([8, 16, 32, 48, 64]))
+    return {
+        "levels": levels,
+        "batch": draw(st.integers(1, 3)),
+        "queries": draw(st.integers(1, 300)),
+        "heads": H,
+        "channels": D,
+        "points": draw(st.integers(1, 8)),
+        "seed": draw(st.integers(0, 2**31 - 1)),
+        "dtype": draw(st.sampled_from([F32, BF16, F16])),
+        "softmax": draw(st.booleans()),
+        "path": draw(st.sampled_from(sorted(PATHS))),
+    }
+
+
+@given(case=cases())
+@settings(max_examples=200, deadline=None, derandomize=True, database=None,
+          suppress_health_check=[HealthCheck.too_slow, HealthCheck.data_too_large,
+                                 HealthCheck.function_scoped_fixture])
+def test_random_shapes_match_oracle(device, case):
+    env = PATHS[case["path"]]
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update(env)
+    try:
+        w = make_workload(0, levels=case["levels"], batch=case["batch"], queries=case["queries"],
+                          heads=case["heads"], channels=case["channels"], points=case["points"],
+                          seed=case["seed"]).to(device, case["dtype"])
+        check_against_oracle(*w.operands(softmax=case["softmax"]), w.grad_output, softmax=case["softmax"],
+                             dtype=case["dtype"], label=str(case))
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
