@@ -272,9 +272,12 @@ def supports_context(context: MSDAContext) -> bool:
     """Whether the HIP kernels take a call with this context.
 
     A ROCm GPU tensor of float32/float16/bfloat16/float64, at most 64 lanes per
-    head (``D / channels_per_lane``; D <= 512 for 16-bit values) and one wave's
-    staged samples within the 64 KiB LDS budget. Mirrors the library's own launch
-    checks, so dispatch reports NoBackendError instead of a launch error.
+    head (``D / channels_per_lane``; D <= 512 for 16-bit values) and one unit's
+    staged samples, locations and weights within the 64 KiB LDS budget of a wave
+    (the library gives a unit more lanes, and a wave fewer units, until a wave
+    fits). Mirrors the library's own launch checks, so dispatch reports
+    NoBackendError instead of a launch error; the location width is taken at its
+    largest (4 bytes, 8 for float64).
     """
     if context.device.type != "cuda" or torch.version.hip is None:
         return False
@@ -289,9 +292,16 @@ def supports_context(context: MSDAContext) -> bool:
     lanes = head_dim // _channels_per_lane(context.dtype, head_dim)
     if lanes > 64:  # noqa: PLR2004
         return False
-    lanes_per_unit = 1 << (lanes - 1).bit_length()
-    staged = 48 if context.dtype == torch.float64 else 32
-    return 16 * context.num_levels + (64 // lanes_per_unit) * samples * staged <= 64 * 1024
+    f64 = context.dtype == torch.float64
+    staged = 48 if f64 else 32
+    value_bytes = torch.empty((), dtype=context.dtype).element_size()
+    loc_bytes = 8 if f64 else 4
+
+    def align16(n: int) -> int:
+        return (n + 15) // 16 * 16
+
+    one_unit = align16(16 * context.num_levels + samples * staged) + align16(samples * 2 * loc_bytes)
+    return one_unit + align16(samples * value_bytes) <= 64 * 1024
 
 
 class Backend:

@@ -2813,16 +2813,24 @@ int make_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, 
                 (long long)D, (long long)lanes, cv, kWave);
   int lh_log2 = 0;
   while ((1 << lh_log2) < lanes) ++lh_log2;
-  const int uw = kWave >> lh_log2;
   // The forward stages 16-bit weight pairs (StagedPk); the backward stages fp32 / fp64.
   const size_t staged = (dtype == MSDA_F64)             ? sizeof(Staged<double>)
                         : (!backward && es == 2 && cv >= 2) ? sizeof(StagedPk)
                                                             : sizeof(Staged<float>);
-  // Per wave: the staged records, and the LDS copy of the units' locations and weights.
-  const size_t raw_wave = size_t(unit_raw_bytes(uw, int(L * P), loc_es, es));
-  const size_t per_wave = size_t(uw) * size_t(L * P) * staged;
   const size_t levels_bytes = sizeof(Level) * size_t(L);
-  auto lds_of = [&](int w) { return ((levels_bytes + per_wave * w + 15) & ~size_t(15)) + raw_wave * w; };
+  // Per wave: the staged records of its units, and the LDS copy of their locations
+  // and weights. When one wave's units do not fit, a unit takes more lanes (the
+  // lanes past the channels stage samples and idle in the gathers), so a wave holds
+  // fewer units.
+  auto lds_for = [&](int lhl, int w) {
+    const int u = kWave >> lhl;
+    const size_t per_wave = size_t(u) * size_t(L * P) * staged;
+    const size_t raw_wave = size_t(unit_raw_bytes(u, int(L * P), loc_es, es));
+    return ((levels_bytes + per_wave * w + 15) & ~size_t(15)) + raw_wave * w;
+  };
+  while (lh_log2 < 6 && lds_for(lh_log2, 1) > kMaxLds) ++lh_log2;
+  const int uw = kWave >> lh_log2;
+  auto lds_of = [&](int w) { return lds_for(lh_log2, w); };
   if (lds_of(1) > kMaxLds)
     return fail(MSDA_ERR_UNSUPPORTED,
                 "msda: %lld samples per (query, head) do not fit the %zu-byte LDS staging of one "

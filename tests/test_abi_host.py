@@ -129,6 +129,43 @@ def test_launch_geometry_rejects_what_the_kernels_do_not_cover(lib):
     assert rc == 1
 
 
+def test_launch_geometry_widens_units_whose_samples_overflow_a_wave(lib):
+    # bf16, D = 8: one lane would serve a unit, so a wave would stage 64 units x 40
+    # samples (77 KB with their locations and weights). The plan gives each unit more
+    # lanes until one wave fits; the backward's grad_sample plan does the same.
+    for backward in (False, True):
+        rc, cpl, lpu, wpb, nb = geometry(lib, 2, (1, 4, 1, 8, 1, 5, 8), backward=backward)
+        assert rc == 0, lib.cdll.msda_last_error()
+        if not backward:
+            assert cpl == 8 and lpu >= 2
+    # Even one unit per wave cannot stage 2048 float32 samples: unsupported, and the
+    # registry's predicate says so before any launch.
+    rc, *_ = geometry(lib, 0, (1, 64, 1, 32, 16, 1, 2048), backward=True)
+    assert rc == 2
+    assert "lds" in lib.cdll.msda_last_error().decode().lower()
+
+
+@pytest.mark.parametrize(
+    ("levels", "points", "dtype", "head_dim", "expected"),
+    [
+        (4, 7, torch.bfloat16, 8, True),
+        (5, 8, torch.float32, 8, True),
+        (1, 1024, torch.float32, 32, True),
+        (1, 2048, torch.float32, 32, False),
+        (1, 1024, torch.float64, 16, False),
+    ],
+)
+def test_backend_predicate_matches_the_lds_budget(levels, points, dtype, head_dim, expected):
+    from deformops_amd.backends.hip._bridge import supports_context  # noqa: PLC0415
+    from deformops_amd.registry import MSDAContext  # noqa: PLC0415
+
+    if torch.version.hip is None:
+        pytest.skip("the predicate is for ROCm builds of torch")
+    context = MSDAContext(device=torch.device("cuda"), num_levels=levels, num_heads=1, num_points=points,
+                          dtype=dtype, sm_version=(9, 5), is_training=True, num_queries=1, head_dim=head_dim)
+    assert supports_context(context) is expected
+
+
 def test_missing_library_raises_kernel_error(monkeypatch, tmp_path):
     from deformops_amd.core.errors import KernelNotProvidedError  # noqa: PLC0415
 

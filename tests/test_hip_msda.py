@@ -127,6 +127,10 @@ SHAPES = [
     pytest.param(((8, 8), (4, 4)), 1, 7, 3, 128, 6, id="d128-p6"),
     pytest.param(((7, 8), (4, 4)), 1, 11, 5, 16, 7, id="odd-heads-p7"),
     pytest.param(((10, 12), (5, 6), (3, 3), (2, 2), (1, 1)), 1, 9, 2, 64, 8, id="five-levels-p8"),
+    # D = 8 with many samples: a unit takes more lanes than its channels need, so
+    # that one wave's staging fits the LDS (found by the hypothesis sweep).
+    pytest.param(((1, 1), (1, 1), (1, 1), (1, 1)), 1, 1, 1, 8, 7, id="d8-p7-tiny"),
+    pytest.param(((9, 11), (5, 6), (3, 3), (2, 2), (1, 1)), 2, 37, 3, 8, 8, id="d8-five-levels-p8"),
 ]
 
 
