@@ -2,8 +2,8 @@
 
 The GPU counterpart of the reference's hypothesis parity test
 (``tests/deformops/test_msda_reference.py:31-88``), widened: batch, heads, head
-width, levels and their shapes, points, queries, value dtype and softmax / linear
-method are drawn together, and every example checks the forward and all three
+width (odd ones included), levels and their shapes, points, queries, value dtype
+(float64 included) and softmax / linear method are drawn together, and every example checks the forward and all three
 gradients against the float64 C oracle with the tolerances of
 ``tests/test_hip_msda.py``. The owner kernel for grad_value (matrix cores or VALU)
 and the bucket sort's counting mode (per-workgroup rows or atomics) are drawn too,
@@ -20,7 +20,7 @@ import torch
 from hypothesis import HealthCheck, given, settings
 from hypothesis import strategies as st
 
-from tests.test_hip_msda import BF16, F16, F32, check_against_oracle
+from tests.test_hip_msda import BF16, F16, F32, F64, check_against_oracle
 from tests.workloads import make_workload
 
 pytestmark = pytest.mark.gpu
@@ -29,6 +29,7 @@ PATHS = {
     "default": {},
     "valu": {"DEFORMOPS_AMD_NO_MFMA": "1"},
     "atomic-sort": {"DEFORMOPS_AMD_ATOMIC_SORT": "1"},
+    "valu-atomic-sort": {"DEFORMOPS_AMD_NO_MFMA": "1", "DEFORMOPS_AMD_ATOMIC_SORT": "1"},
 }
 
 
@@ -36,8 +37,8 @@ PATHS = {
 def cases(draw):
     L = draw(st.integers(1, 5))
     levels = tuple((draw(st.integers(1, 40)), draw(st.integers(1, 40))) for _ in range(L))
-    H = draw(st.sampled_from([1, 2, 3, 4, 8]))
-    D = draw(st.sampled_from([8, 16, 32, 48, 64]))
+    H = draw(st.sampled_from([1, 2, 3, 4, 8, 16]))
+    D = draw(st.sampled_from([7, 8, 16, 24, 32, 48, 64]))
     return {
         "levels": levels,
         "batch": draw(st.integers(1, 3)),
@@ -46,7 +47,7 @@ def cases(draw):
         "channels": D,
         "points": draw(st.integers(1, 8)),
         "seed": draw(st.integers(0, 2**31 - 1)),
-        "dtype": draw(st.sampled_from([F32, BF16, F16])),
+        "dtype": draw(st.sampled_from([F32, BF16, F16, F64])),
         "softmax": draw(st.booleans()),
         "path": draw(st.sampled_from(sorted(PATHS))),
     }
