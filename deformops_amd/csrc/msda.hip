@@ -265,14 +265,27 @@ template <typename T> __device__ inline float dot2_16(uint32_t a, uint32_t b, fl
 template <int CTRL> __device__ inline float quad_perm(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
 }
-constexpr int kQuadXor1 = 0xb1;  // quad_perm [1, 0, 3, 2]
-constexpr int kQuadXor2 = 0x4e;  // quad_perm [2, 3, 0, 1]
+constexpr int kQuadXor1 = 0xb1;       // quad_perm [1, 0, 3, 2]
+constexpr int kQuadXor2 = 0x4e;       // quad_perm [2, 3, 0, 1]
+constexpr int kRowHalfMirror = 0x141;  // lane i of each 8 reads lane 7 - i
+constexpr int kRowMirror = 0x140;      // lane i of each 16 reads lane 15 - i
 
+// Sum / max over a unit's lh lanes (a power of two), left in every lane. float units
+// of up to 16 lanes use DPP moves: after the quad steps each group of 4 holds its
+// total, and a mirror pairs every lane with one of the other group (the sums are
+// the same in every lane: each step adds two equal-ordered values).
 template <typename A> __device__ inline A unit_sum(A v, int lh) {
   if constexpr (__is_same(A, float)) {
     if (lh <= 4) {
       if (lh >= 2) v += quad_perm<kQuadXor1>(v);
       if (lh >= 4) v += quad_perm<kQuadXor2>(v);
+      return v;
+    }
+    if (lh <= 16) {
+      v += quad_perm<kQuadXor1>(v);
+      v += quad_perm<kQuadXor2>(v);
+      v += quad_perm<kRowHalfMirror>(v);
+      if (lh >= 16) v += quad_perm<kRowMirror>(v);
       return v;
     }
   }
@@ -284,6 +297,13 @@ template <typename A> __device__ inline A unit_max(A v, int lh) {
     if (lh <= 4) {
       if (lh >= 2) v = fmax(v, quad_perm<kQuadXor1>(v));
       if (lh >= 4) v = fmax(v, quad_perm<kQuadXor2>(v));
+      return v;
+    }
+    if (lh <= 16) {
+      v = fmax(v, quad_perm<kQuadXor1>(v));
+      v = fmax(v, quad_perm<kQuadXor2>(v));
+      v = fmax(v, quad_perm<kRowHalfMirror>(v));
+      if (lh >= 16) v = fmax(v, quad_perm<kRowMirror>(v));
       return v;
     }
   }
