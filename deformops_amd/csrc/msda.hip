@@ -2137,9 +2137,10 @@ __device__ inline MfmaCorners<typename MfmaOp<T>::W> mfma_kblock_a(const MfmaTil
   return cr;
 }
 
-template <typename T, int NB>
+// TAIL: a tile's last K-blocks, whose second K-step may hold no candidate.
+template <typename T, int NB, bool TAIL = false>
 __device__ inline void mfma_kblock_b(const MfmaCorners<typename MfmaOp<T>::W>& cr, int lane, const unsigned char* gst,
-                                     unsigned char* wt, f32x4_v (&acc)[4][NB]) {
+                                     unsigned char* wt, f32x4_v (&acc)[4][NB], int ksteps = 2) {
   using Op = MfmaOp<T>;
   using V = typename Op::V;
   using W = typename Op::W;
@@ -2151,6 +2152,8 @@ __device__ inline void mfma_kblock_b(const MfmaCorners<typename MfmaOp<T>::W>& c
   const u32x4_v zero = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
+    if constexpr (TAIL)
+      if (ks >= ksteps) break;  // wave-uniform: the K-step holds no candidate
     wave_lds_order();
 #pragma unroll
     for (int z = 0; z < 4 * kWBytes / (kWave * 16); ++z)
@@ -2199,6 +2202,11 @@ __device__ inline void mfma_kblock_b(const MfmaCorners<typename MfmaOp<T>::W>& c
       }
     }
   }
+}
+
+// K-steps of K-block kb that hold candidates (the rest would add zeros).
+__device__ inline int mfma_ksteps(const MfmaTile& t, uint32_t kb) {
+  return t.ncand > kb * kMfmaK + kMfmaKStep ? 2 : 1;
 }
 
 // The K-blocks kb0, kb0 + kbstep, ... of one tile into acc (zeroed here). Block j's
@@ -2251,10 +2259,10 @@ __device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, con
     if (two) mfma_load_meta<T, TL, SOFTMAX>(t, eb, mb);
     const auto c0 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ma, rows, lane, gst);
     if (two) mfma_load_rows<T, NB>(t, eb, lane, rows);
-    mfma_kblock_b<T, NB>(c0, lane, gst, wt, acc);
+    mfma_kblock_b<T, NB, true>(c0, lane, gst, wt, acc, mfma_ksteps(t, kb));
     if (two) {
       const auto c1 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, mb, rows, lane, gst);
-      mfma_kblock_b<T, NB>(c1, lane, gst, wt, acc);
+      mfma_kblock_b<T, NB, true>(c1, lane, gst, wt, acc, mfma_ksteps(t, kb + uint32_t(kbstep)));
     }
   }
 }
