@@ -2969,7 +2969,8 @@ size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
 
 int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, int64_t L,
                        int64_t P, int loc_dtype, const void* const* vec_ptrs, int n_vec,
-                       const void* grad_attn, size_t lds_limit, int cus, BackwardPlan* plan) {
+                       const void* grad_attn, size_t lds_limit, int cus, BackwardPlan* plan,
+                       bool accumulate = false) {
   // vec_ptrs: value, grad_output, grad_value (channel vectors), then the locations.
   const int n_chan = std::min(n_vec, 3);
   int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_chan, &plan->sample, elem_size(loc_dtype));
@@ -3068,9 +3069,11 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   bg.div_lp = make_fastdiv(uint32_t(L * P));
   bg.div_p = make_fastdiv(uint32_t(P));
   // Grouped bucketing: groups of 4 samples, LDS counters for every bucket, and the
-  // saved keys (16-bit when every key fits) inside grad_value.
+  // saved keys (16-bit when every key fits) inside grad_value. Not when grad_value's
+  // contents are to be accumulated into: the per-sample passes recompute the keys.
   const void* loc_ptr = n_vec > 3 ? vec_ptrs[3] : nullptr;
-  bg.group4 = (L * P) % 4 == 0 && P % 4 == 0 && plan->bucket && (loc_ptr == nullptr || aligned(loc_ptr, 16));
+  bg.group4 = !accumulate && (L * P) % 4 == 0 && P % 4 == 0 && plan->bucket &&
+              (loc_ptr == nullptr || aligned(loc_ptr, 16));
   bg.key_bytes = 4 * tiles_bound < 0xffff ? 2 : 4;
   if (B * H * samples_bh * bg.key_bytes > B * S * H * D * es) bg.group4 = 0;
   if (!bg.group4) bg.key_bytes = 0;
@@ -3390,7 +3393,7 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   BackwardPlan plan;
   rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
                           loc_dtype, vec, 4, grad_attention_weights, device_lds_limit(), device_cus(),
-                          &plan);
+                          &plan, accumulate);
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,

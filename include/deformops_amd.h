@@ -93,18 +93,22 @@ int msda_forward(const void* value, int value_dtype,
  *   grad_sampling_locations  [B, Q, H, L, P, 2]  loc_dtype
  *   grad_attention_weights   [B, Q, H, L * P]    value_dtype (w.r.t. the logits
  *                                                 under MSDA_SOFTMAX)
- * Every element of grad_value is written exactly once, by the one thread that
- * owns it, from an fp32 (fp64 for MSDA_F64) register sum of all its contributions;
- * with MSDA_ACCUMULATE_GRAD_VALUE the previous contents are added to that sum. No
+ * Every element of grad_value gets its gradient from one owner, which sums all its
+ * contributions in fp32 (fp64 for MSDA_F64) and stores once; with
+ * MSDA_ACCUMULATE_GRAD_VALUE the previous contents are added to that sum. No
  * atomics touch grad_value, it needs no zero-fill, and there is no float32 copy.
- * The order in which an element's contributions are summed, and so the last bits of
- * grad_value, may vary between runs. The other two gradients are written in full,
- * zeros included. While the call runs, grad_sampling_locations and
- * grad_attention_weights serve as its scratch (a bucket sort of the samples by
- * pyramid tile); they are overwritten with the gradients before it completes. So
- * the call needs no memory beyond its outputs, and the three gradient buffers
- * must not alias each other or the inputs. grad_sampling_locations must be 4-byte
- * aligned.
+ * Where the sort keeps per-workgroup counts (the default when the scratch has
+ * room) the summation order is fixed and results repeat bit for bit; with its
+ * atomic fallback the order, and so the last bits of grad_value, may vary between
+ * runs. The other two gradients are written in full, zeros included. While the call
+ * runs, its outputs serve as its scratch (a bucket sort of the samples by pyramid
+ * tile): grad_sampling_locations holds the sorted sample indices,
+ * grad_attention_weights the bucket counters, and grad_value the samples' keys
+ * until the owners overwrite it (with MSDA_ACCUMULATE_GRAD_VALUE the keys are
+ * recomputed instead, and grad_value holds only its previous contents);
+ * all three hold their gradients when the call completes. So the call needs no
+ * memory beyond its outputs, and the three gradient buffers must not alias each
+ * other or the inputs. grad_sampling_locations must be 4-byte aligned.
  *
  * Replaces deformops_cuda::msda_fp32acc[_softmax]_backward
  * (sources/deformops/backends/cuda/_schema.py:24-29, include/msda_boxed.cuh:32-53,

@@ -209,6 +209,44 @@ def test_counters_that_do_not_fit_fall_back_to_the_owner_kernel(device, dtype, q
                              label=f"2x1024 level, {queries} queries")
 
 
+@pytest.mark.parametrize(
+    ("dtype", "sizes"),
+    [
+        pytest.param(BF16, {}, id="bf16-matrix-cores"),
+        pytest.param(F32, {}, id="f32-matrix-cores"),
+        pytest.param(F32, {"channels": 24, "points": 3}, id="f32-valu-per-sample-sort"),
+    ],
+)
+def test_accumulate_flag_adds_into_grad_value(device, dtype, sizes):
+    """MSDA_ACCUMULATE_GRAD_VALUE through the C ABI: grad_value = previous + gradient,
+    with the other two gradients as without the flag."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    lib = _lib.load()
+    w = make_workload(2, batch=1, queries=1500, **sizes).to(device, dtype)
+    value, shapes, starts, loc, attn = w.operands()
+    B, S, H, D, Q, L, P = w.sizes
+    stream = torch.cuda.current_stream()
+    codes = (_lib.DTYPE_CODES[value.dtype], _lib.DTYPE_CODES[loc.dtype], _lib.INDEX_CODES[shapes.dtype])
+
+    def backward(grad_value, flags):
+        gl, ga = torch.empty_like(loc), torch.empty_like(attn)
+        lib.check(lib.backward(value.data_ptr(), codes[0], shapes.data_ptr(), starts.data_ptr(), codes[2],
+                               loc.data_ptr(), codes[1], attn.data_ptr(), w.grad_output.data_ptr(),
+                               grad_value.data_ptr(), gl.data_ptr(), ga.data_ptr(),
+                               B, S, H, D, Q, L, P, flags, stream.cuda_stream))
+        torch.cuda.synchronize()
+        return grad_value, gl, ga
+
+    plain = backward(torch.empty_like(value), 0)
+    previous = torch.randn(value.shape, generator=torch.Generator().manual_seed(3)).to(device, dtype)
+    added = backward(previous.clone(), _lib.FLAG_ACCUMULATE_GRAD_VALUE)
+    expected = previous.double() + plain[0].double()
+    assert rel_err(added[0], expected.cpu()) <= BWD_TOL[dtype]
+    torch.testing.assert_close(added[1], plain[1], rtol=0, atol=0)
+    torch.testing.assert_close(added[2], plain[2], rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("dtype", [BF16, F16, F32], ids=["bf16", "f16", "f32"])
 def test_samples_piled_on_one_tile(device, dtype):
     """Every sample of every query lands near one pixel: one tile owns them all, so a
