@@ -97,10 +97,10 @@ int msda_forward(const void* value, int value_dtype,
  * contributions in fp32 (fp64 for MSDA_F64) and stores once; with
  * MSDA_ACCUMULATE_GRAD_VALUE the previous contents are added to that sum. No
  * atomics touch grad_value, it needs no zero-fill, and there is no float32 copy.
- * Where the sort keeps per-workgroup counts (the default when the scratch has
- * room) the summation order is fixed and results repeat bit for bit; with its
- * atomic fallback the order, and so the last bits of grad_value, may vary between
- * runs. The other two gradients are written in full, zeros included. While the call
+ * The order in which an element's contributions are summed follows the order the
+ * bucket sort gives the samples, which depends on the order of its LDS atomics
+ * across waves; so the last bits of grad_value may vary between runs. The other two
+ * gradients are written in full, zeros included. While the call
  * runs, its outputs serve as its scratch (a bucket sort of the samples by pyramid
  * tile): grad_sampling_locations holds the sorted sample indices,
  * grad_attention_weights the bucket counters, and grad_value the samples' keys
