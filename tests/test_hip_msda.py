@@ -247,6 +247,55 @@ def test_accumulate_flag_adds_into_grad_value(device, dtype, sizes):
     torch.testing.assert_close(added[2], plain[2], rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("dtype", [BF16, F32], ids=["bf16", "f32"])
+def test_calls_replay_from_a_hip_graph(device, dtype):
+    """The forward and backward C-ABI calls launch kernels only (no allocation, no
+    memset), so a caller can capture them in a HIP graph. Each replay, with eager
+    work in between that poisons the outputs, must give the eager results."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    lib = _lib.load()
+    w = make_workload(2, batch=1, queries=2000).to(device, dtype)
+    value, shapes, starts, loc, attn = w.operands(softmax=True)
+    B, S, H, D, Q, L, P = w.sizes
+    codes = (_lib.DTYPE_CODES[value.dtype], _lib.DTYPE_CODES[loc.dtype], _lib.INDEX_CODES[shapes.dtype])
+    out = torch.empty((B, Q, H * D), dtype=dtype, device=device)
+    gv, gl, ga = torch.empty_like(value), torch.empty_like(loc), torch.empty_like(attn)
+
+    def calls() -> None:
+        st = torch.cuda.current_stream().cuda_stream
+        lib.check(lib.forward(value.data_ptr(), codes[0], shapes.data_ptr(), starts.data_ptr(), codes[2],
+                              loc.data_ptr(), codes[1], attn.data_ptr(), out.data_ptr(),
+                              B, S, H, D, Q, L, P, _lib.FLAG_SOFTMAX, st))
+        lib.check(lib.backward(value.data_ptr(), codes[0], shapes.data_ptr(), starts.data_ptr(), codes[2],
+                               loc.data_ptr(), codes[1], attn.data_ptr(), w.grad_output.data_ptr(),
+                               gv.data_ptr(), gl.data_ptr(), ga.data_ptr(),
+                               B, S, H, D, Q, L, P, _lib.FLAG_SOFTMAX, st))
+
+    calls()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in (out, gv, gl, ga)]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        calls()
+    for _ in range(3):
+        for t in (out, gv, gl, ga):
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, want in zip((out, gv, gl, ga), eager):
+            assert not torch.isnan(got).any()
+            # grad_value's summation order may differ between runs; the rest is exact.
+            tol = BWD_TOL[dtype] if got is gv else 0.0
+            assert rel_err(got, want.double().cpu()) <= tol
+
+
 @pytest.mark.parametrize("dtype", [BF16, F16, F32], ids=["bf16", "f16", "f32"])
 def test_samples_piled_on_one_tile(device, dtype):
     """Every sample of every query lands near one pixel: one tile owns them all, so a
