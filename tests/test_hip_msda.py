@@ -296,6 +296,57 @@ def test_calls_replay_from_a_hip_graph(device, dtype):
             assert rel_err(got, want.double().cpu()) <= tol
 
 
+def test_concurrent_calls_from_two_threads_on_two_streams(device):
+    """The library keeps no state between calls (scratch lives in each call's outputs,
+    errors are thread-local): two host threads, each calling the backward on its own
+    stream with its own workload, get the sequential results."""
+    import threading  # noqa: PLC0415
+
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    lib = _lib.load()
+    works = [make_workload(2, batch=1, queries=1800, seed=s).to(device, dt) for s, dt in ((1, BF16), (2, F32))]
+
+    def backward(w, stream):
+        value, shapes, starts, loc, attn = w.operands()
+        B, S, H, D, Q, L, P = w.sizes
+        gv, gl, ga = torch.empty_like(value), torch.empty_like(loc), torch.empty_like(attn)
+        lib.check(lib.backward(value.data_ptr(), _lib.DTYPE_CODES[value.dtype], shapes.data_ptr(),
+                               starts.data_ptr(), _lib.INDEX_CODES[shapes.dtype], loc.data_ptr(),
+                               _lib.DTYPE_CODES[loc.dtype], attn.data_ptr(), w.grad_output.data_ptr(),
+                               gv.data_ptr(), gl.data_ptr(), ga.data_ptr(), B, S, H, D, Q, L, P, 0,
+                               stream.cuda_stream))
+        return gv, gl, ga
+
+    stream0 = torch.cuda.current_stream()
+    expected = [backward(w, stream0) for w in works]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    results: list = [None, None]
+    errors: list = []
+
+    def run(i):
+        try:
+            with torch.cuda.stream(streams[i]):
+                results[i] = [backward(works[i], streams[i]) for _ in range(4)]
+        except Exception as exc:  # noqa: BLE001 - reported below
+            errors.append(exc)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    assert not errors, errors
+    for i, w in enumerate(works):
+        dt = w.value.dtype
+        for gv, gl, ga in results[i]:
+            assert rel_err(gv, expected[i][0].double().cpu()) <= BWD_TOL[dt]
+            torch.testing.assert_close(gl, expected[i][1], rtol=0, atol=0)
+            torch.testing.assert_close(ga, expected[i][2], rtol=0, atol=0)
+
+
 @pytest.mark.parametrize("dtype", [BF16, F16, F32], ids=["bf16", "f16", "f32"])
 def test_samples_piled_on_one_tile(device, dtype):
     """Every sample of every query lands near one pixel: one tile owns them all, so a
