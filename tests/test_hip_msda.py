@@ -209,22 +209,25 @@ def test_counters_that_do_not_fit_fall_back_to_the_owner_kernel(device, dtype, q
                              label=f"2x1024 level, {queries} queries")
 
 
+@pytest.mark.parametrize("softmax", [False, True], ids=["linear", "softmax"])
 @pytest.mark.parametrize(
-    ("dtype", "sizes"),
+    ("dtype", "cfg", "sizes"),
     [
-        pytest.param(BF16, {}, id="bf16-matrix-cores"),
-        pytest.param(F32, {}, id="f32-matrix-cores"),
-        pytest.param(F32, {"channels": 24, "points": 3}, id="f32-valu-per-sample-sort"),
+        pytest.param(BF16, 2, {"queries": 1500}, id="bf16-matrix-cores"),
+        pytest.param(F32, 2, {"queries": 1500}, id="f32-matrix-cores"),
+        pytest.param(F32, 2, {"queries": 1500, "channels": 24, "points": 3}, id="f32-valu-per-sample-sort"),
+        pytest.param(BF16, 1, {"batch": 2}, id="bf16-decoder-standby"),
     ],
 )
-def test_accumulate_flag_adds_into_grad_value(device, dtype, sizes):
+def test_accumulate_flag_adds_into_grad_value(device, dtype, cfg, sizes, softmax):
     """MSDA_ACCUMULATE_GRAD_VALUE through the C ABI: grad_value = previous + gradient,
     with the other two gradients as without the flag."""
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
 
     lib = _lib.load()
-    w = make_workload(2, batch=1, queries=1500, **sizes).to(device, dtype)
-    value, shapes, starts, loc, attn = w.operands()
+    w = make_workload(cfg, **{"batch": 1, **sizes}).to(device, dtype)
+    value, shapes, starts, loc, attn = w.operands(softmax=softmax)
+    method = _lib.FLAG_SOFTMAX if softmax else 0
     B, S, H, D, Q, L, P = w.sizes
     stream = torch.cuda.current_stream()
     codes = (_lib.DTYPE_CODES[value.dtype], _lib.DTYPE_CODES[loc.dtype], _lib.INDEX_CODES[shapes.dtype])
@@ -238,9 +241,9 @@ def test_accumulate_flag_adds_into_grad_value(device, dtype, sizes):
         torch.cuda.synchronize()
         return grad_value, gl, ga
 
-    plain = backward(torch.empty_like(value), 0)
+    plain = backward(torch.empty_like(value), method)
     previous = torch.randn(value.shape, generator=torch.Generator().manual_seed(3)).to(device, dtype)
-    added = backward(previous.clone(), _lib.FLAG_ACCUMULATE_GRAD_VALUE)
+    added = backward(previous.clone(), method | _lib.FLAG_ACCUMULATE_GRAD_VALUE)
     expected = previous.double() + plain[0].double()
     assert rel_err(added[0], expected.cpu()) <= BWD_TOL[dtype]
     torch.testing.assert_close(added[1], plain[1], rtol=0, atol=0)
