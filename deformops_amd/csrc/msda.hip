@@ -129,11 +129,6 @@ template <int CV> struct Chan<float, CV> {
     for (int i = 0; i < CV; ++i) r.w[i] = __float_as_uint(v[i]);
     *reinterpret_cast<R*>(p) = r;
   }
-  static __device__ inline void atomic_add(char* p, const float (&g)[CV], float s) {
-#pragma unroll
-    for (int i = 0; i < CV; ++i)
-      __builtin_amdgcn_global_atomic_fadd_f32(reinterpret_cast<float*>(p) + i, g[i] * s);
-  }
 };
 
 template <int CV> struct Chan<double, CV> {
@@ -164,28 +159,15 @@ template <int CV> struct Chan<double, CV> {
     }
     *reinterpret_cast<R*>(p) = r;
   }
-  static __device__ inline void atomic_add(char* p, const double (&g)[CV], double s) {
-#pragma unroll
-    for (int i = 0; i < CV; ++i)
-      __builtin_amdgcn_global_atomic_fadd_f64(reinterpret_cast<double*>(p) + i, g[i] * s);
-  }
 };
 
-// bf16 and f16 share the packing; only the conversions and the atomic differ.
+// bf16 and f16 share the packing; only the conversions differ.
 template <typename T, int CV> struct Chan16 {
   static constexpr bool kBf16 = sizeof(T) == 2 && __is_same(T, bf16_t);
   using R = Raw<2 * CV>;
   static __device__ inline float lo(uint32_t w) { return kBf16 ? bf16_lo(w) : f16_bits(w & 0xffffu); }
   static __device__ inline float hi(uint32_t w) { return kBf16 ? bf16_hi(w) : f16_bits(w >> 16); }
   static __device__ inline uint32_t pack(float a, float b) { return kBf16 ? pack_bf16(a, b) : pack_f16(a, b); }
-  static __device__ inline void atomic2(uint32_t* p, uint32_t packed) {
-    if constexpr (kBf16)
-      __builtin_amdgcn_global_atomic_fadd_v2bf16(reinterpret_cast<bf16x2_v*>(p),
-                                                 __builtin_bit_cast(bf16x2_v, packed));
-    else
-      __builtin_amdgcn_global_atomic_fadd_v2f16(reinterpret_cast<f16x2_v*>(p),
-                                                __builtin_bit_cast(f16x2_v, packed));
-  }
   static __device__ inline void from_raw(const R& r, float (&v)[CV]) {
     if constexpr (CV == 1) {
       v[0] = lo(r.h);
@@ -228,19 +210,6 @@ template <typename T, int CV> struct Chan16 {
       for (int i = 0; i < CV / 2; ++i) r.w[i] = pack(v[2 * i], v[2 * i + 1]);
     }
     *reinterpret_cast<R*>(p) = r;
-  }
-  static __device__ inline void atomic_add(char* p, const float (&g)[CV], float s) {
-    if constexpr (CV == 1) {
-      // The packed atomic covers the aligned dword; the neighbour gets +0.
-      const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-      const float x = g[0] * s;
-      const uint32_t packed = (a & 2) ? pack(0.0f, x) : pack(x, 0.0f);
-      atomic2(reinterpret_cast<uint32_t*>(a & ~uintptr_t(3)), packed);
-    } else {
-#pragma unroll
-      for (int i = 0; i < CV / 2; ++i)
-        atomic2(reinterpret_cast<uint32_t*>(p) + i, pack(g[2 * i] * s, g[2 * i + 1] * s));
-    }
   }
 };
 template <int CV> struct Chan<bf16_t, CV> : Chan16<bf16_t, CV> {};
