@@ -7,9 +7,11 @@ the caller allows compiling); there is no fallback path.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
+from collections.abc import Iterator
 from pathlib import Path
 
 import torch
@@ -20,16 +22,20 @@ __all__ = [
     "ABI_VERSION",
     "DTYPE_CODES",
     "FLAG_ACCUMULATE_GRAD_VALUE",
+    "FLAG_GRAD_VALUE_ATOMIC",
     "FLAG_SOFTMAX",
+    "PATH_ATOMIC_SORT",
+    "PATH_NO_MFMA",
     "INDEX_CODES",
     "EXPORTED_SYMBOLS",
     "Library",
     "library_path",
     "load",
+    "path_override",
 ]
 
 #: MSDA_ABI_VERSION this binding was written for.
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 #: enum msda_dtype.
 DTYPE_CODES: dict[torch.dtype, int] = {
@@ -43,6 +49,10 @@ INDEX_CODES: dict[torch.dtype, int] = {torch.int64: 0, torch.int32: 1}
 #: enum msda_flags.
 FLAG_SOFTMAX = 1
 FLAG_ACCUMULATE_GRAD_VALUE = 2
+FLAG_GRAD_VALUE_ATOMIC = 4
+#: enum msda_path_bits.
+PATH_NO_MFMA = 1
+PATH_ATOMIC_SORT = 2
 
 #: Every function the header declares.
 EXPORTED_SYMBOLS = (
@@ -51,6 +61,7 @@ EXPORTED_SYMBOLS = (
     "msda_last_error",
     "msda_abi_version",
     "msda_launch_geometry",
+    "msda_set_path_override",
 )
 
 _P = ctypes.c_void_p
@@ -86,8 +97,14 @@ class Library:
             ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_I), ctypes.POINTER(_L),
         ]
         lib.msda_launch_geometry.restype = _I
+        lib.msda_set_path_override.argtypes = [_I]
+        lib.msda_set_path_override.restype = _I
         self.forward = lib.msda_forward
         self.backward = lib.msda_backward
+
+    def set_path_override(self, paths: int) -> int:
+        """Force kernel paths (``PATH_*`` bits, 0 for the library's choice); returns the previous bits."""
+        return int(self.cdll.msda_set_path_override(paths))
 
     def abi_version(self) -> int:
         return int(self.cdll.msda_abi_version())
@@ -166,3 +183,14 @@ def load(*, download: bool | None = None, compile: bool | str | None = None) -> 
             raise KernelUnavailableError(msg)
         _loaded = library
         return library
+
+
+@contextlib.contextmanager
+def path_override(paths: int) -> Iterator[None]:
+    """Run the enclosed calls on the kernel paths ``paths`` forces (tests of every path)."""
+    library = load()
+    previous = library.set_path_override(paths)
+    try:
+        yield
+    finally:
+        library.set_path_override(previous)

@@ -39,6 +39,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <stdlib.h>
 #include <type_traits>
 #include <math.h>
@@ -215,16 +216,6 @@ template <typename T, int CV> struct Chan16 {
 template <int CV> struct Chan<bf16_t, CV> : Chan16<bf16_t, CV> {};
 template <int CV> struct Chan<f16_t, CV> : Chan16<f16_t, CV> {};
 
-// acc + a.lo * b.lo + a.hi * b.hi for two packed 16-bit pairs (v_dot2_f32_bf16 /
-// v_dot2_f32_f16).
-template <typename T> __device__ inline float dot2_16(uint32_t a, uint32_t b, float acc) {
-  if constexpr (__is_same(T, bf16_t))
-    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a), __builtin_bit_cast(bf16x2_v, b), acc,
-                                           false);
-  else
-    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_v, a), __builtin_bit_cast(f16x2_v, b), acc, false);
-}
-
 // ---------------------------------------------------------------------------
 // Cross-lane reductions inside the LH lanes of one unit (LH a power of two, the
 // unit's lanes contiguous and aligned). Every lane of the wave must call them.
@@ -283,6 +274,53 @@ template <typename A> __device__ inline A unit_max(A v, int lh) {
 __device__ inline float exp_acc(float x) { return __expf(x); }
 __device__ inline double exp_acc(double x) { return exp(x); }
 
+// grad_value[p + i] += w * g[i] for the CV channels at byte address p, with global
+// atomics in the value dtype: fp32 and fp64 adds, packed bf16 / f16 pair adds
+// (CV >= 2 keeps p 4-byte aligned), and for a single 16-bit channel a 32-bit
+// compare-and-swap on the aligned word that holds it (the word never leaves the
+// element's page, and the swap leaves the other half as it finds it).
+template <typename T, int CV>
+__device__ inline void atomic_add_channels(char* p, typename Elem<T>::acc w, const typename Elem<T>::acc (&g)[CV]) {
+  if constexpr (std::is_same_v<T, float> || std::is_same_v<T, double>) {
+#pragma unroll
+    for (int i = 0; i < CV; ++i) unsafeAtomicAdd(reinterpret_cast<T*>(p) + i, w * g[i]);
+  } else if constexpr (CV >= 2) {
+#pragma unroll
+    for (int i = 0; i < CV / 2; ++i) {
+      if constexpr (std::is_same_v<T, bf16_t>) {
+        const bf16x2_v v = {static_cast<__bf16>(w * g[2 * i]), static_cast<__bf16>(w * g[2 * i + 1])};
+        __builtin_amdgcn_global_atomic_fadd_v2bf16(reinterpret_cast<bf16x2_v*>(p) + i, v);
+      } else {
+        const f16x2_v v = {static_cast<_Float16>(w * g[2 * i]), static_cast<_Float16>(w * g[2 * i + 1])};
+        __builtin_amdgcn_global_atomic_fadd_v2f16(reinterpret_cast<f16x2_v*>(p) + i, v);
+      }
+    }
+  } else {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    uint32_t* word = reinterpret_cast<uint32_t*>(a & ~uintptr_t(3));
+    const int shift = (a & 2) ? 16 : 0;
+    const float add = w * g[0];
+    uint32_t old = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (;;) {
+      const uint32_t bits = (old >> shift) & 0xffffu;
+      float cur;
+      uint32_t nb;
+      if constexpr (std::is_same_v<T, bf16_t>) {
+        cur = __uint_as_float(bits << 16);
+        nb = __builtin_bit_cast(uint16_t, static_cast<__bf16>(cur + add));
+      } else {
+        cur = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+        nb = __builtin_bit_cast(uint16_t, static_cast<_Float16>(cur + add));
+      }
+      const uint32_t want = (old & ~(0xffffu << shift)) | (nb << shift);
+      if (__hip_atomic_compare_exchange_strong(word, &old, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT))
+        break;
+    }
+  }
+}
+
+
 // ---------------------------------------------------------------------------
 // Problem description, passed by value to every kernel.
 
@@ -304,6 +342,7 @@ struct Problem {
   int blocks_per_batch;
   int num_blocks;
   int loc_piece, attn_piece;  // bytes per lane access copying a wave's records to LDS
+  int atomic_gv;              // backward: grad_sample scatters grad_value with atomics
 };
 
 // One pyramid level as the kernels use it. A level whose table entry does not fit
@@ -314,19 +353,13 @@ struct alignas(16) Level {
 };
 
 // A staged sample: four corner byte offsets (inside one batch image, with the
-// unit's head folded in) and four weights (bilinear * attention, zero for a corner
-// outside the level). In the backward the weights slot is reused for the reduced
-// G_c once phase 2 has read it.
+// unit's head folded in) and four weights (bilinear * attention in the accumulation
+// type, fp32 for every 16-bit value dtype; zero for a corner outside the level). In
+// the backward the weights slot is reused for the reduced G_c once phase 2 has read
+// it.
 template <typename A> struct alignas(16) Staged {
   uint32_t off[4];
   A w[4];
-};
-
-// The forward's staged sample for 16-bit values: the four corner offsets and the
-// weight pairs (w00, w01), (w10, w11) packed in the value dtype.
-struct alignas(8) StagedPk {
-  uint32_t off[4];
-  uint32_t w01, w23;
 };
 
 __device__ inline void load_levels(const Problem& p, Level* levels) {
@@ -344,6 +377,41 @@ __device__ inline void load_levels(const Problem& p, Level* levels) {
     const bool ok = h > 0 && w > 0 && st >= 0 && h <= p.S && w <= p.S && st + h * w <= p.S;
     levels[i] = ok ? Level{int(h), int(w), int(st), 1} : Level{1, 1, 0, 0};
   }
+}
+
+// Whether this thread's levels (i = threadIdx.x, + blockDim.x, ...) share positions
+// of S with another valid level. The reference's validator calls such a table
+// malformed (core/sanitize.py:395-436), but its eager and atomic paths sum every
+// level's contribution into a shared element; the backward does the same by
+// scattering grad_value with atomics when any level overlaps. Callers OR the
+// result over the workgroup with overlap_flag_raise.
+__device__ inline bool thread_levels_overlap(const Level* levels, int L) {
+  bool any = false;
+  for (int i = threadIdx.x; i < L && !any; i += blockDim.x) {
+    const Level a = levels[i];
+    if (!a.ok) continue;
+    const int64_t a0 = a.start, a1 = a0 + int64_t(a.h) * a.w;
+    for (int j = 0; j < L; ++j) {
+      const Level b = levels[j];
+      const int64_t b0 = b.start, b1 = b0 + int64_t(b.h) * b.w;
+      if (j != i && b.ok && a0 < b1 && b0 < a1) {
+        any = true;
+        break;
+      }
+    }
+  }
+  return any;
+}
+
+// A workgroup's "levels overlap" flag in LDS: cleared by thread 0 before a barrier,
+// raised (rarely) by the threads that find an overlap between that barrier and the
+// next, read by every thread after the next.
+__device__ inline int* overlap_flag() {
+  __shared__ int flag;
+  return &flag;
+}
+__device__ inline void overlap_flag_raise(const Level* levels, int L) {
+  if (thread_levels_overlap(levels, L)) atomicOr(overlap_flag(), 1);
 }
 
 // Geometry of one sample. Contraction is off so that pixel = loc * size - 0.5 and
@@ -509,9 +577,7 @@ __device__ inline UnitRaw copy_unit_records(const Problem& p, const LaneMap& m, 
 
 // Phase 1, shared by both directions: stage every sample of the lane's unit and
 // return the unit's softmax statistics (max and 1 / sum of exp), if any.
-// With PACK (16-bit value dtypes), `wst` holds StagedPk records instead: the weight
-// pairs rounded to the value dtype, for the forward's packed dot products.
-template <typename T, typename TL, bool SOFTMAX, bool PACK = false>
+template <typename T, typename TL, bool SOFTMAX>
 __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const Level* levels,
                                      const UnitRaw& raw, Staged<typename Elem<T>::acc>* wst,
                                      typename Elem<T>::acc& smax,
@@ -543,23 +609,14 @@ __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const L
                                   levels[s / p.P], head_bytes, pos_bytes);
     A a = load_acc(attn + s);
     if constexpr (SOFTMAX) a = exp_acc(a - smax) * sinv;
-    if constexpr (PACK) {
-      StagedPk st;
+    Staged<A> st;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) st.off[c] = g.off[c];
-      st.w01 = Chan16<T, 2>::pack(g.w00 * a, g.w01 * a);
-      st.w23 = Chan16<T, 2>::pack(g.w10 * a, g.w11 * a);
-      reinterpret_cast<StagedPk*>(wst)[s * m.uw_count + m.uw] = st;
-    } else {
-      Staged<A> st;
-#pragma unroll
-      for (int c = 0; c < 4; ++c) st.off[c] = g.off[c];
-      st.w[0] = g.w00 * a;
-      st.w[1] = g.w01 * a;
-      st.w[2] = g.w10 * a;
-      st.w[3] = g.w11 * a;
-      wst[s * m.uw_count + m.uw] = st;
-    }
+    for (int c = 0; c < 4; ++c) st.off[c] = g.off[c];
+    st.w[0] = g.w00 * a;
+    st.w[1] = g.w01 * a;
+    st.w[2] = g.w10 * a;
+    st.w[3] = g.w11 * a;
+    wst[s * m.uw_count + m.uw] = st;
   }
 }
 
@@ -570,23 +627,18 @@ template <typename T, typename TL, int CV, bool SOFTMAX>
 __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel(const Problem p) {
   using A = typename Elem<T>::acc;
   constexpr int ES = Elem<T>::size;
-  // 16-bit values: two corners per packed dot product. v_perm_b32 pairs channel i
-  // of corners (0, 1), and of (2, 3); v_dot2_f32_{bf16,f16} multiplies the pair by
-  // the staged weight pair (rounded to the value dtype) and adds to the fp32 sum:
-  // one instruction per two products, no widening.
-  constexpr bool kPacked = ES == 2 && CV >= 2;
   extern __shared__ __align__(16) unsigned char smem[];
   Level* levels = reinterpret_cast<Level*>(smem);
   const LaneMap m = map_lane(p);
   const int LP = p.L * p.P;
-  constexpr size_t kRec = kPacked ? sizeof(StagedPk) : sizeof(Staged<A>);
+  constexpr size_t kRec = sizeof(Staged<A>);
   Staged<A>* wst = reinterpret_cast<Staged<A>*>(smem + sizeof(Level) * p.L + kRec * m.wave * m.uw_count * LP);
   const size_t raw_at = (sizeof(Level) * p.L + kRec * (blockDim.x / kWave) * m.uw_count * LP + 15) & ~size_t(15);
   const UnitRaw raw = copy_unit_records<T, TL>(p, m, smem + raw_at);
   load_levels(p, levels);
   __syncthreads();
   A smax, sinv;
-  stage_samples<T, TL, SOFTMAX, kPacked>(p, m, levels, raw, wst, smax, sinv);
+  stage_samples<T, TL, SOFTMAX>(p, m, levels, raw, wst, smax, sinv);
   __syncthreads();
 
   if (!m.unit_ok || m.t * CV >= p.D) return;
@@ -595,36 +647,19 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
   A acc[CV];
 #pragma unroll
   for (int i = 0; i < CV; ++i) acc[i] = A(0);
-  if constexpr (kPacked) {
-    using R = typename Chan<T, CV>::R;
-    const StagedPk* wpk = reinterpret_cast<const StagedPk*>(wst);
+  // Every corner value is widened to the accumulation type and multiplied by its
+  // weight (attention * bilinear, kept in that type) into the sum, as the
+  // reference's kernels do with their fp32 accumulator.
 #pragma unroll 2
-    for (int s = 0; s < LP; ++s) {
-      const StagedPk st = wpk[s * m.uw_count + m.uw];
-      R v[4];
+  for (int s = 0; s < LP; ++s) {
+    const Staged<A> st = wst[s * m.uw_count + m.uw];
+    A v[4][CV];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v[c] = *reinterpret_cast<const R*>(img + (st.off[c] + lane_bytes));
-      const uint32_t w01 = st.w01, w23 = st.w23;
+    for (int c = 0; c < 4; ++c) Chan<T, CV>::load(img + (st.off[c] + lane_bytes), v[c]);
 #pragma unroll
-      for (int i = 0; i < CV / 2; ++i) {
-        acc[2 * i] = dot2_16<T>(__builtin_amdgcn_perm(v[1].w[i], v[0].w[i], 0x05040100u), w01, acc[2 * i]);
-        acc[2 * i + 1] = dot2_16<T>(__builtin_amdgcn_perm(v[1].w[i], v[0].w[i], 0x07060302u), w01, acc[2 * i + 1]);
-        acc[2 * i] = dot2_16<T>(__builtin_amdgcn_perm(v[3].w[i], v[2].w[i], 0x05040100u), w23, acc[2 * i]);
-        acc[2 * i + 1] = dot2_16<T>(__builtin_amdgcn_perm(v[3].w[i], v[2].w[i], 0x07060302u), w23, acc[2 * i + 1]);
-      }
-    }
-  } else {
-#pragma unroll 2
-    for (int s = 0; s < LP; ++s) {
-      const Staged<A> st = wst[s * m.uw_count + m.uw];
-      A v[4][CV];
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) Chan<T, CV>::load(img + (st.off[c] + lane_bytes), v[c]);
-#pragma unroll
-      for (int c = 0; c < 4; ++c)
-#pragma unroll
-        for (int i = 0; i < CV; ++i) acc[i] = fma(st.w[c], v[c][i], acc[i]);
-    }
+      for (int i = 0; i < CV; ++i) acc[i] = fma(st.w[c], v[c][i], acc[i]);
   }
   Chan<T, CV>::store(p.out + (m.gunit * p.D + m.t * CV) * ES, acc);
 }
@@ -862,15 +897,22 @@ __device__ inline typename Elem<T>::acc unit_weight(const T* unit_attn, int LP, 
   }
 }
 
-// Shared set-up of the bucketing kernels and the owner: the level table and the
-// tiles in LDS. Returns the tile count of one (b, h) (-1: too many).
+// Shared set-up of the bucketing kernels and the owners: the level table and the
+// tiles in LDS. Returns the tile count of one (b, h), or -1 when there are too many
+// tiles or when valid levels overlap (`overlap` then says so): the sort and the
+// owners then stand aside, and msda_grad_sample_kernel scatters grad_value with
+// atomics.
 __device__ inline int64_t load_tiles(const Problem& p, const BwdGeom& bg, Level* levels,
-                                     LevelTiles* lt, int64_t* total_out) {
+                                     LevelTiles* lt, int64_t* total_out, bool* overlap = nullptr) {
+  if (threadIdx.x == 0) *overlap_flag() = 0;
   load_levels(p, levels);
   __syncthreads();
+  overlap_flag_raise(levels, p.L);
   if (threadIdx.x == 0) *total_out = plan_tiles(p, bg, levels, lt);
   __syncthreads();
-  return *total_out;
+  const bool any = *overlap_flag() != 0;
+  if (overlap) *overlap = any;
+  return any ? -1 : *total_out;
 }
 
 // The per-workgroup count rows of the chunked bucket sort, nkeys ints for each
@@ -1382,19 +1424,24 @@ __global__ __launch_bounds__(256) void msda_softmax_stats_kernel(const Problem p
   }
 }
 
-// Zeroes grad_value[b, pos, :, :] at every position no valid level covers; the tile
-// owners write all the others.
+// Zeroes grad_value[b, pos, :, :] at every position no valid level covers (every
+// position when levels overlap); the tile owners write all the others.
 template <typename T>
 __global__ __launch_bounds__(256) void msda_gap_zero_kernel(const Problem p) {
   extern __shared__ __align__(16) unsigned char smem[];
   Level* levels = reinterpret_cast<Level*>(smem);
+  if (threadIdx.x == 0) *overlap_flag() = 0;
   load_levels(p, levels);
   __syncthreads();
+  overlap_flag_raise(levels, p.L);
+  __syncthreads();
+  // Overlapping levels: every position starts at zero for the atomic scatter.
+  const bool overlap = *overlap_flag() != 0;
   const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (idx >= int64_t(p.B) * p.S) return;
   const int pos = int(idx % p.S);
   bool covered = false;
-  for (int l = 0; l < p.L && !covered; ++l) {
+  for (int l = 0; l < p.L && !covered && !overlap; ++l) {
     const Level lv = levels[l];
     covered = lv.ok && pos >= lv.start && int64_t(pos) < int64_t(lv.start) + int64_t(lv.h) * lv.w;
   }
@@ -1428,7 +1475,8 @@ template <> struct PieceOf<16> { using type = u32x4_v; };
 template <typename T, int CVR> using Piece = typename PieceOf<Elem<T>::size * CVR>::type;
 
 // How the owner kernel adds one corner record (weight w, staged grad_out piece g)
-// into its CVR accumulators: acc[c] += w * g[c].
+// into its CVR accumulators: acc[c] += w * g[c], with g widened to the accumulation
+// type and w kept in it (fp32 for 16-bit values).
 template <typename T, int CVR> struct OwnerAdd {
   using A = typename Elem<T>::acc;
   using Rec = TileRec<A>;
@@ -1440,35 +1488,6 @@ template <typename T, int CVR> struct OwnerAdd {
     for (int c = 0; c < CVR; ++c) acc[c] = fma(r.w, g[c], acc[c]);
   }
 };
-
-// bfloat16 pairs: v_dot2c_f32_bf16 against the packed weights (w, 0) and (0, w)
-// adds w * g for the low and the high channel of a pair in one instruction each,
-// with no widening of g. The weight is rounded to bfloat16 once per record (round
-// to nearest even, unbiased, at most 2^-9 relative); products and sums stay fp32.
-// A non-finite grad_out channel also turns its pair neighbour's sum non-finite
-// (0 * inf), where widening would keep the neighbour finite.
-template <int CVR> struct OwnerAddBf16 {
-  struct alignas(8) Rec {
-    uint32_t wb;   // the weight as bfloat16, in the low half
-    uint32_t off;  // byte offset of the record's staged grad_out row
-  };
-  static __device__ inline Rec make(float w, uint32_t off) {
-    return Rec{uint32_t(__builtin_bit_cast(uint16_t, static_cast<__bf16>(w))), off};
-  }
-  static __device__ inline void add(float (&acc)[CVR], const Rec& r, const Piece<bf16_t, CVR>& pc) {
-    const Raw<2 * CVR> g = __builtin_bit_cast(Raw<2 * CVR>, pc);
-    const bf16x2_v lo = __builtin_bit_cast(bf16x2_v, r.wb), hi = __builtin_bit_cast(bf16x2_v, r.wb << 16);
-#pragma unroll
-    for (int i = 0; i < CVR / 2; ++i) {
-      const bf16x2_v pair = __builtin_bit_cast(bf16x2_v, g.w[i]);
-      acc[2 * i] = __builtin_amdgcn_fdot2_f32_bf16(pair, lo, acc[2 * i], false);
-      acc[2 * i + 1] = __builtin_amdgcn_fdot2_f32_bf16(pair, hi, acc[2 * i + 1], false);
-    }
-  }
-};
-template <> struct OwnerAdd<bf16_t, 2> : OwnerAddBf16<2> {};
-template <> struct OwnerAdd<bf16_t, 4> : OwnerAddBf16<4> {};
-template <> struct OwnerAdd<bf16_t, 8> : OwnerAddBf16<8> {};
 
 // Exclusive prefix sum of n <= 4 * 64 counters by one wave (four per lane, DPP scan
 // of the lane totals); writes start[0..n] and clears the counters.
@@ -1835,19 +1854,25 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
 // none, so a sample adds exactly its corners in the tile). The candidates come in
 // K-blocks of 64, one per lane; light tasks run one per wave, heavy ones split their
 // K-blocks over the workgroup's four waves. Per K-block a wave stages the 64
-// grad_out rows in its own LDS (row-major), and per K-step of 32 candidates scatters
-// their corner weights into four zeroed weight tiles and reads the operands back.
-//   - bf16 / f16: v_mfma_f32_16x16x32_{bf16,f16}, one per sub-tile and 16 channels and
-//     K-step; A (position-major weight tiles) with ds_read_b128, B (grad_out, K-major)
-//     with two ds_read_b64_tr_b16 per 16 channels. The weight enters the MFMA rounded
-//     to 16 bits (nearest even).
-//   - float: v_mfma_f32_16x16x4_f32, eight per sub-tile and 16 channels and K-step;
-//     candidate-major weight tiles and rows padded by 16 bytes, read with ds_read_b32.
-//     The weight enters exact.
-// Products and sums are fp32. Waves do not wait for each other inside a task; the
-// loads of the next K-block (and the entries of the one after) are in flight while a
-// K-block computes. A split task's four partial sums meet in LDS at its end and wave
-// w writes sub-tile w.
+// grad_out rows in its own LDS (row-major, bf16), and per K-step of 32 candidates
+// scatters their corner weights into zeroed weight tiles and reads the operands
+// back: A (position-major weight tiles) with ds_read_b128, B (grad_out, K-major)
+// with two ds_read_b64_tr_b16 per 16 channels.
+//
+// Every value dtype runs v_mfma_f32_16x16x32_bf16 on operands split into two bf16
+// parts, x = hi + lo + e: hi is x rounded to bf16 (nearest even) and lo the rest
+// rounded again, so |e| <= 2^-16 |x|.
+//   - W (fp32 attention * bilinear) is split for every dtype: two weight tiles per
+//     sub-tile, W_hi and W_lo.
+//   - G is exact in bf16 for bf16 values. f16 and float rows are split too, into
+//     two staged row buffers; f16's 11 significant bits fit hi + lo exactly.
+//   - Per sub-tile, 16 channels and K-step the MFMAs add W_hi G_hi + W_lo G_hi, and
+//     W_hi G_lo when G is split. Products are exact and sums fp32, so a product's
+//     relative error is at most 2^-16 (bf16), 2^-15 (f16: the dropped W_lo G_lo) and
+//     3 * 2^-16 (float: W_lo G_lo and the two splits).
+// Waves do not wait for each other inside a task; the loads of the next K-block (and
+// the entries of the one after) are in flight while a K-block computes. A split
+// task's four partial sums meet in LDS at its end and wave w writes sub-tile w.
 //
 // Operand layouts of v_mfma_f32_16x16x32 (wave64; lane l, g = l / 16, i = l % 16):
 //   A: halves A[i][8 g .. 8 g + 7];  B: halves B[8 g .. 8 g + 7][i];
@@ -1858,10 +1883,10 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
 // G[8 g + 4 t + j][16 nb + i]: half t of its B operand for channels 16 nb .. + 15.
 //
 // A non-finite grad_out channel reaches every position of the tiles its sample is a
-// candidate of (0 * inf), not only the sample's corners.
+// candidate of (0 * inf), not only the sample's corners. The low part of a
+// non-finite value is zero, so an infinite product stays infinite.
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
 typedef float f32x4_v __attribute__((ext_vector_type(4)));
 typedef short i16x4_v __attribute__((ext_vector_type(4)));
 
@@ -1871,40 +1896,34 @@ constexpr int kMfmaK = 64;        // candidates per K-block: one per lane, two M
 constexpr int kMfmaKStep = 32;    // the MFMA's K
 constexpr int kMfmaMaxNb = 4;     // 16-channel column blocks: D <= 64
 
-// One 16 x 32 weight tile (16 positions, one K-step of candidates) in the value
-// dtype's width, and the LDS stride of a staged grad_out row. float rows get 16
-// bytes of padding: the fp32 MFMA's B operand reads four rows at once.
-constexpr int mfma_wbytes(int es) { return 16 * kMfmaKStep * es; }
-constexpr int mfma_row_stride(int nb, int es) { return 16 * nb * es + (es == 4 ? 16 : 0); }
+// One 16 x 32 bf16 weight tile (16 positions, one K-step of candidates); a K-step
+// has four sub-tiles of hi tiles, then four of lo tiles. A staged grad_out row holds
+// 16 nb bf16 channels.
+constexpr int kMfmaWBytes = 16 * kMfmaKStep * 2;
+constexpr int kMfmaLoTiles = 4 * kMfmaWBytes;  // offset of the lo tiles
+constexpr int mfma_row_bytes(int nb) { return 16 * nb * 2; }
+// Whether grad_out rows of a value dtype are split into hi and lo (f16 and float).
+constexpr bool mfma_split_rows(int es, bool bf16) { return !(es == 2 && bf16); }
 
-// The MFMA of each value dtype. 16-bit values: v_mfma_f32_16x16x32_{bf16,f16}, the
-// weight rounded to the value dtype (W). float: v_mfma_f32_16x16x4_f32, eight per
-// K-step, the weight exact.
-template <typename T> struct MfmaOp;
-template <> struct MfmaOp<bf16_t> {
-  using V = bf16x8_v;
-  using W = uint16_t;
-  static __device__ inline f32x4_v mma(V a, V b, f32x4_v c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-  static __device__ inline W round(float w) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(w)); }
-};
-template <> struct MfmaOp<f16_t> {
-  using V = f16x8_v;
-  using W = uint16_t;
-  static __device__ inline f32x4_v mma(V a, V b, f32x4_v c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-  static __device__ inline W round(float w) { return __builtin_bit_cast(uint16_t, static_cast<_Float16>(w)); }
-};
-template <> struct MfmaOp<float> {
-  using V = float;
-  using W = uint32_t;
-  static __device__ inline f32x4_v mma(V a, V b, f32x4_v c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-  }
-  static __device__ inline W round(float w) { return __builtin_bit_cast(uint32_t, w); }
-};
+__device__ inline f32x4_v mfma_bf16(bf16x8_v a, bf16x8_v b, f32x4_v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// The bf16 parts of x (see above); lo is zero for a non-finite x.
+__device__ inline void split_bf16(float x, uint16_t* hi, uint16_t* lo) {
+  const __bf16 h = static_cast<__bf16>(x);
+  *hi = __builtin_bit_cast(uint16_t, h);
+  const __bf16 r = static_cast<__bf16>(x - static_cast<float>(h));
+  *lo = __builtin_isfinite(x) ? __builtin_bit_cast(uint16_t, r) : uint16_t(0);
+}
+// Two floats to packed (hi, lo) bf16 pairs, element 0 in the low halves.
+__device__ inline void split_bf16_pair(float a, float b, uint32_t* hi, uint32_t* lo) {
+  uint16_t ha, la, hb, lb;
+  split_bf16(a, &ha, &la);
+  split_bf16(b, &hb, &lb);
+  *hi = uint32_t(ha) | (uint32_t(hb) << 16);
+  *lo = uint32_t(la) | (uint32_t(lb) << 16);
+}
 
 // A wave-uniform value moved to a scalar register (it is the same in every lane).
 __device__ inline int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -1915,11 +1934,13 @@ __device__ inline i16x4_v lds_read_tr16(const unsigned char* p) {
       reinterpret_cast<__attribute__((address_space(3))) i16x4_v*>(reinterpret_cast<uintptr_t>(p)));
 }
 
-// Per-wave LDS of the matrix-core kernel: the staged rows and the four weight
-// tiles during a tile, the wave's partial sums at its end.
-size_t mfma_wave_bytes(int64_t D, int es) {
-  const size_t work = size_t(kMfmaK) * size_t(mfma_row_stride(int(D / 16), es)) +
-                      4 * size_t(mfma_wbytes(es));  // rows + 4 weight tiles
+// Per-wave LDS of the matrix-core kernel: the staged rows (one or two bf16 buffers)
+// and the eight weight tiles during a tile, the wave's partial sums at its end.
+size_t mfma_rows_bytes(int64_t D, bool split) {
+  return size_t(kMfmaK) * size_t(mfma_row_bytes(int(D / 16))) * (split ? 2 : 1);
+}
+size_t mfma_wave_bytes(int64_t D, bool split) {
+  const size_t work = mfma_rows_bytes(D, split) + 8 * size_t(kMfmaWBytes);
   const size_t partial = 4 * size_t(D / 16) * kWave * 16;
   return std::max(work, partial);
 }
@@ -1930,8 +1951,8 @@ size_t mfma_head_bytes(int64_t L) {
   return at + 16;
 }
 
-size_t mfma_lds_bytes(int64_t L, int64_t D, int es) {
-  return mfma_head_bytes(L) + kMfmaWaves * mfma_wave_bytes(D, es);
+size_t mfma_lds_bytes(int64_t L, int64_t D, bool split) {
+  return mfma_head_bytes(L) + kMfmaWaves * mfma_wave_bytes(D, split);
 }
 
 // The candidates of one tile: ranges of the entry list (the tile's own
@@ -2038,32 +2059,68 @@ __device__ inline void mfma_load_rows(const MfmaTile& t, uint32_t e, int lane, M
 }
 
 // One K-block of one wave, in two parts. Part A: the candidate's corners (as LDS
-// byte offsets of their weights in the four weight tiles, -1 outside the tile, and
-// the weights rounded to the value dtype), and the block's 64 grad_out rows into
-// LDS, after which the row registers are free for the next block's loads. Part B:
-// per MFMA K-step (the candidates of lanes 0-31, then 32-63) scatter the corner
-// weights into the zeroed weight tiles and run the four sub-tiles' MFMAs.
-template <typename W> struct MfmaCorners {
+// byte offsets of their weights in the hi weight tiles, -1 outside the tile, and the
+// weights' bf16 parts), and the block's 64 grad_out rows into LDS as bf16 (hi and
+// lo buffers when split), after which the row registers are free for the next
+// block's loads. Part B: per MFMA K-step (the candidates of lanes 0-31, then 32-63)
+// scatter the corner weights into the weight tiles, run the sub-tiles' MFMAs, and
+// clear the scattered entries again. The tiles are zeroed once (mfma_zero_tiles) and
+// are all zeros between K-steps: clearing at most eight 2-byte entries per lane costs
+// far less LDS bandwidth than zeroing the 8 KB of tiles per K-step. A wave's LDS
+// instructions execute in order, so the clears land after the operand reads.
+struct MfmaCorners {
   int o[4];
-  W w[4];
+  uint16_t hi[4], lo[4];
 };
 
+// A staged 16-byte piece of a grad_out row as bf16: copied (bf16), or split into
+// hi and lo parts (f16: 8 channels, 16 bytes each; float: 4 channels, 8 bytes each).
+template <typename T>
+__device__ inline void mfma_stage_piece(const u32x4_v& v, unsigned char* hi, unsigned char* lo) {
+  if constexpr (std::is_same_v<T, bf16_t>) {
+    *reinterpret_cast<u32x4_v*>(hi) = v;
+  } else if constexpr (std::is_same_v<T, f16_t>) {
+    u32x4_v h, l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t hw, lw;
+      split_bf16_pair(f16_bits(v[i] & 0xffffu), f16_bits(v[i] >> 16), &hw, &lw);
+      h[i] = hw;
+      l[i] = lw;
+    }
+    *reinterpret_cast<u32x4_v*>(hi) = h;
+    *reinterpret_cast<u32x4_v*>(lo) = l;
+  } else {
+    u32x2_v h, l;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      uint32_t hw, lw;
+      split_bf16_pair(__uint_as_float(v[2 * i]), __uint_as_float(v[2 * i + 1]), &hw, &lw);
+      h[i] = hw;
+      l[i] = lw;
+    }
+    *reinterpret_cast<u32x2_v*>(hi) = h;
+    *reinterpret_cast<u32x2_v*>(lo) = l;
+  }
+}
+
 template <typename T, typename TL, int NB, bool SOFTMAX>
-__device__ inline MfmaCorners<typename MfmaOp<T>::W> mfma_kblock_a(const MfmaTile& t, const Level& lv, uint32_t kb,
-                                                                  uint32_t e, const MfmaMeta<T, TL>& d,
-                                                                  const MfmaRows<mfma_pieces<T, NB>()>& rows,
-                                                                  int lane, unsigned char* gst) {
-  using Op = MfmaOp<T>;
+__device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, uint32_t kb, uint32_t e,
+                                            const MfmaMeta<T, TL>& d, const MfmaRows<mfma_pieces<T, NB>()>& rows,
+                                            int lane, unsigned char* gst) {
   constexpr int ES = int(sizeof(T));
   constexpr int kPieces = mfma_pieces<T, NB>();
-  constexpr int kRowStride = mfma_row_stride(NB, ES);
-  constexpr int kWBytes = mfma_wbytes(ES);
+  constexpr int kRowBytes = mfma_row_bytes(NB);
+  constexpr int kStagedPiece = 16 * 2 / ES;  // bf16 bytes a 16-byte piece becomes
+  constexpr size_t kLoRows = size_t(kMfmaK) * kRowBytes;
   const int kc = lane & (kMfmaKStep - 1);
   const uint32_t c = kb * kMfmaK + uint32_t(lane);
-  MfmaCorners<typename Op::W> cr;
-  float w[4] = {0.f, 0.f, 0.f, 0.f};
+  MfmaCorners cr;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) cr.o[k] = -1;
+  for (int k = 0; k < 4; ++k) {
+    cr.o[k] = -1;
+    cr.hi[k] = cr.lo[k] = 0;
+  }
   if (c < t.ncand) {
     const Geom<float> g = geometry<float>(to_acc(d.loc.x), to_acc(d.loc.y), lv, 0u, 1u);
     float a;
@@ -2084,93 +2141,95 @@ __device__ inline MfmaCorners<typename MfmaOp<T>::W> mfma_kblock_a(const MfmaTil
     for (int k = 0; k < 4; ++k) {
       const int y = y0 + (k >> 1), x = x0 + (k & 1);
       // Position (y, x) of the tile: sub-tile (y / 4) * 2 + x / 4, row (y % 4) * 4 + x % 4
-      // of its weight tile, which is position-major for 16-bit values ([16][32]) and
-      // candidate-major for float ([32][16]), the layouts the MFMAs read.
+      // of its position-major [16][32] weight tile.
       if (m[k] && y >= 0 && x >= 0 && t.r0 + y < t.r1 && t.c0 + x < t.c1) {
         const int pos = (y & 3) * 4 + (x & 3);
-        cr.o[k] = ((y >> 2) * 2 + (x >> 2)) * kWBytes + (ES == 4 ? (kc * 16 + pos) * 4 : pos * (2 * kMfmaKStep) + kc * 2);
-        w[k] = wb[k] * a;
+        cr.o[k] = ((y >> 2) * 2 + (x >> 2)) * kMfmaWBytes + pos * (2 * kMfmaKStep) + kc * 2;
+        split_bf16(wb[k] * a, &cr.hi[k], &cr.lo[k]);
       }
     }
   }
-#pragma unroll
-  for (int k = 0; k < 4; ++k) cr.w[k] = Op::round(w[k]);
   wave_lds_order();  // after the previous K-block's operand reads
   const u32x4_v zero = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int j = 0; j < kPieces; ++j) {
     const int f = lane + kWave * j, row = f / kPieces, pc = f - row * kPieces;
     const bool ok = kb * kMfmaK + uint32_t(row) < t.ncand;  // past the end: zero rows
-    *reinterpret_cast<u32x4_v*>(gst + row * kRowStride + pc * 16) = ok ? rows.piece[j] : zero;
+    unsigned char* dst = gst + row * kRowBytes + pc * kStagedPiece;
+    mfma_stage_piece<T>(ok ? rows.piece[j] : zero, dst, dst + kLoRows);
   }
   return cr;
 }
 
 // TAIL: a tile's last K-blocks, whose second K-step may hold no candidate.
 template <typename T, int NB, bool TAIL = false>
-__device__ inline void mfma_kblock_b(const MfmaCorners<typename MfmaOp<T>::W>& cr, int lane, const unsigned char* gst,
-                                     unsigned char* wt, f32x4_v (&acc)[4][NB], int ksteps = 2) {
-  using Op = MfmaOp<T>;
-  using V = typename Op::V;
-  using W = typename Op::W;
-  constexpr int ES = int(sizeof(T));
-  constexpr int kRowBytes = mfma_row_stride(NB, ES);
-  constexpr int kWBytes = mfma_wbytes(ES);
+__device__ inline void mfma_kblock_b(const MfmaCorners& cr, int lane, const unsigned char* gst, unsigned char* wt,
+                                     f32x4_v (&acc)[4][NB], int ksteps = 2) {
+  constexpr bool kSplit = !std::is_same_v<T, bf16_t>;
+  constexpr int kRowBytes = mfma_row_bytes(NB);
+  constexpr size_t kLoRows = size_t(kMfmaK) * kRowBytes;
   const int half = lane >> 5;
   const int g16 = lane >> 4, i16 = lane & 15;
-  const u32x4_v zero = {0u, 0u, 0u, 0u};
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     if constexpr (TAIL)
       if (ks >= ksteps) break;  // wave-uniform: the K-step holds no candidate
     wave_lds_order();
+    if (half == ks) {
 #pragma unroll
-    for (int z = 0; z < 4 * kWBytes / (kWave * 16); ++z)
-      *reinterpret_cast<u32x4_v*>(wt + (z * kWave + lane) * 16) = zero;
+      for (int k = 0; k < 4; ++k)
+        if (cr.o[k] >= 0) {
+          *reinterpret_cast<uint16_t*>(wt + cr.o[k]) = cr.hi[k];
+          *reinterpret_cast<uint16_t*>(wt + kMfmaLoTiles + cr.o[k]) = cr.lo[k];
+        }
+    }
+    wave_lds_order();
+    bf16x8_v bh[NB], bl[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const unsigned char* src =
+          gst + (kMfmaKStep * ks + 8 * g16 + i16 / 4) * kRowBytes + (16 * nb + 4 * (i16 & 3)) * 2;
+      bh[nb] = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(lds_read_tr16(src), lds_read_tr16(src + 4 * kRowBytes),
+                                                                     0, 1, 2, 3, 4, 5, 6, 7));
+      if constexpr (kSplit)
+        bl[nb] = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(lds_read_tr16(src + kLoRows),
+                                                                       lds_read_tr16(src + kLoRows + 4 * kRowBytes),
+                                                                       0, 1, 2, 3, 4, 5, 6, 7));
+    }
+    const int aoff = i16 * (2 * kMfmaKStep) + g16 * 16;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const bf16x8_v ah = __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const u32x4_v*>(wt + st * kMfmaWBytes + aoff));
+      const bf16x8_v al =
+          __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const u32x4_v*>(wt + kMfmaLoTiles + st * kMfmaWBytes + aoff));
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        if constexpr (kSplit) acc[st][nb] = mfma_bf16(ah, bl[nb], acc[st][nb]);
+        acc[st][nb] = mfma_bf16(al, bh[nb], acc[st][nb]);
+        acc[st][nb] = mfma_bf16(ah, bh[nb], acc[st][nb]);
+      }
+    }
     wave_lds_order();
     if (half == ks) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        if (cr.o[k] >= 0) *reinterpret_cast<W*>(wt + cr.o[k]) = cr.w[k];
-    }
-    wave_lds_order();
-    if constexpr (ES == 4) {
-      // v_mfma_f32_16x16x4_f32, lane l (g = l / 16, i = l % 16): A[i][g] = the weight of
-      // candidate 4 kk + g at position i (candidate-major tiles: conflict-free reads),
-      // B[g][i] = channel 16 nb + i of that candidate's grad_out row; C as above.
-#pragma unroll
-      for (int kk = 0; kk < kMfmaKStep / 4; ++kk) {
-        const int row = kMfmaKStep * ks + 4 * kk + g16;
-        float bv[NB];
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          bv[nb] = *reinterpret_cast<const float*>(gst + row * kRowBytes + (16 * nb + i16) * 4);
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const float av = *reinterpret_cast<const float*>(wt + st * kWBytes + ((4 * kk + g16) * 16 + i16) * 4);
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) acc[st][nb] = Op::mma(av, bv[nb], acc[st][nb]);
+        if (cr.o[k] >= 0) {
+          *reinterpret_cast<uint16_t*>(wt + cr.o[k]) = 0;
+          *reinterpret_cast<uint16_t*>(wt + kMfmaLoTiles + cr.o[k]) = 0;
         }
-      }
-    } else {
-      V bv[NB];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const unsigned char* src =
-            gst + (kMfmaKStep * ks + 8 * g16 + i16 / 4) * kRowBytes + (16 * nb + 4 * (i16 & 3)) * 2;
-        const i16x4_v t0 = lds_read_tr16(src);
-        const i16x4_v t1 = lds_read_tr16(src + 4 * kRowBytes);
-        bv[nb] = __builtin_bit_cast(V, __builtin_shufflevector(t0, t1, 0, 1, 2, 3, 4, 5, 6, 7));
-      }
-      const int aoff = i16 * (2 * kMfmaKStep) + g16 * 16;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const V av = __builtin_bit_cast(V, *reinterpret_cast<const u32x4_v*>(wt + st * kWBytes + aoff));
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) acc[st][nb] = Op::mma(av, bv[nb], acc[st][nb]);
-      }
     }
   }
+}
+
+// Zeroes a wave's eight weight tiles (once per wave, and again after its LDS served
+// for partial sums).
+__device__ inline void mfma_zero_tiles(unsigned char* wt, int lane) {
+  const u32x4_v zero = {0u, 0u, 0u, 0u};
+  wave_lds_order();
+#pragma unroll
+  for (int z = 0; z < 8 * kMfmaWBytes / (kWave * 16); ++z)
+    *reinterpret_cast<u32x4_v*>(wt + (z * kWave + lane) * 16) = zero;
+  wave_lds_order();
 }
 
 // K-steps of K-block kb that hold candidates (the rest would add zeros).
@@ -2263,8 +2322,11 @@ __device__ inline void mfma_store_subtile(const Problem& p, const Level& lv, con
   }
 }
 
-// Workgroups per CU the register budget of the matrix-core kernel allows.
-constexpr int mfma_blocks_per_cu(int nb) { return nb == 1 ? 4 : nb == 2 ? 3 : 2; }
+// Workgroups per CU the register budget of the matrix-core kernel allows (float
+// values prefetch twice the row bytes of 16-bit ones).
+constexpr int mfma_blocks_per_cu(int nb, int es) {
+  return es == 4 ? (nb == 1 ? 3 : 2) : (nb == 1 ? 4 : nb == 2 ? 3 : 2);
+}
 
 constexpr int kMfmaMaxRegions = 16;  // regions per axis at most
 constexpr int kMfmaTable = 1024;      // entries of a queue's prefix table at most
@@ -2308,14 +2370,12 @@ __device__ inline int region_first_tile(int r, int n, int extent, int ntiles) {
 // (pair, level) maps a queue position to its task. When the table would not fit,
 // queue x holds the x-th eighth of each level's tasks (b, tile, h) in raster order.
 template <typename T, typename TL, int NB, bool SOFTMAX>
-__global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void msda_grad_value_mfma_kernel(
+__global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(sizeof(T)))) void msda_grad_value_mfma_kernel(
     const Problem p, const BwdGeom bg, int* __restrict__ buckets,
-    const uint32_t* __restrict__ entries, const int accumulate) {
+    const uint32_t* __restrict__ entries, const int accumulate, const int table_cap) {
   constexpr int D = 16 * NB;
   constexpr int ES = int(sizeof(T));
   extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ int table[kMfmaTable + 1];  // per (pair, level): prefix count of chunks
-  __shared__ int ntab[kMfmaTable];       // per (pair, level): tasks
   __shared__ int wave_sums[kMfmaWaves];
   __shared__ int grid_s[2];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
@@ -2335,21 +2395,27 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
   at = (at + 15) & ~size_t(15);
   int64_t* total = reinterpret_cast<int64_t*>(smem + at);  // [0]: tiles, [1]: the fetched task
   at += 16;
-  constexpr size_t kRowsBytes = size_t(kMfmaK) * size_t(mfma_row_stride(NB, ES));
-  constexpr size_t kWaveBytes = std::max(kRowsBytes + 4 * size_t(mfma_wbytes(ES)), size_t(4 * NB * kWave * 16));
+  constexpr bool kSplit = !std::is_same_v<T, bf16_t>;
+  constexpr size_t kRowsBytes = size_t(kMfmaK) * size_t(mfma_row_bytes(NB)) * (kSplit ? 2 : 1);
+  constexpr size_t kWaveBytes = std::max(kRowsBytes + 8 * size_t(kMfmaWBytes), size_t(4 * NB * kWave * 16));
   unsigned char* region0 = smem + at;
-  unsigned char* gst = region0 + size_t(wave) * kWaveBytes;  // grad_out rows
-  unsigned char* wt = gst + kRowsBytes;                      // four weight tiles
+  unsigned char* gst = region0 + size_t(wave) * kWaveBytes;  // grad_out rows (hi, then lo)
+  unsigned char* wt = gst + kRowsBytes;                      // eight weight tiles (hi, then lo)
+  // Per (pair, level) of this XCD's queue: prefix count of chunks, and tasks.
+  int* table = reinterpret_cast<int*>(region0 + size_t(kMfmaWaves) * kWaveBytes);
+  int* ntab = table + table_cap + 1;
 
-  const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
+  bool overlap;
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total, &overlap);
   if (!accumulate) {
     // grad_value at positions no valid level covers is zero (the tiles own all the
-    // others, so this never meets their stores).
+    // others, so this never meets their stores); when levels overlap, every
+    // position starts at zero for the atomic scatter.
     const int64_t n = int64_t(p.B) * p.S;
     for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + tid; idx < n; idx += int64_t(gridDim.x) * blockDim.x) {
       const int pos = int(idx % p.S);
       bool covered = false;
-      for (int l = 0; l < p.L && !covered; ++l) {
+      for (int l = 0; l < p.L && !covered && !overlap; ++l) {
         const Level lv = levels[l];
         covered = lv.ok && pos >= lv.start && int64_t(pos) < int64_t(lv.start) + int64_t(lv.h) * lv.w;
       }
@@ -2393,7 +2459,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
   const int64_t npairs = int64_t(p.B) * R * R;
   const int64_t pa = xcd * npairs / kXcds, pb = (xcd + 1) * npairs / kXcds;
   const int64_t nentries = (pb - pa) * p.L;
-  const bool regional = nentries <= kMfmaTable;
+  const bool regional = nentries <= table_cap;
   int64_t queue_len = 0;
   if (regional) {
     // Chunks per (pair, level), then their exclusive prefix sums: four entries a thread.
@@ -2433,6 +2499,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
   }
   __syncthreads();
   const int g16 = lane >> 4, i16 = lane & 15;
+  mfma_zero_tiles(wt, lane);
 
   // Thread 0 takes chunks from the queue and publishes them in chunk_s: entry i
   // (-1: the queue is empty) and its tasks [first, last). Regional chunks of light
@@ -2575,6 +2642,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB)) void ms
       }
       mfma_store_subtile<T, NB>(p, lv, t, b, h, wave, sum, g16, i16, accumulate, gv);
       __syncthreads();  // the partial sums are read before the next tile reuses the LDS
+      mfma_zero_tiles(wt, lane);
     }
     __syncthreads();  // every wave is done with the chunk before the next one is published
   }
@@ -2653,20 +2721,39 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
       (sizeof(Level) * p.L + sizeof(Staged<A>) * (blockDim.x / kWave) * m.uw_count * LP + 15) & ~size_t(15);
   const UnitRaw raw = copy_unit_records<T, TL>(p, m, smem + raw_at);
 
+  if (threadIdx.x == 0) *overlap_flag() = 0;
   load_levels(p, levels);
   __syncthreads();
+  overlap_flag_raise(levels, p.L);
   A smax, sinv;
   stage_samples<T, TL, SOFTMAX>(p, m, levels, raw, wst, smax, sinv);
   __syncthreads();
+  // grad_value by atomics: asked for, or levels overlap (the sort and the owners then
+  // only zeroed grad_value).
+  const bool scatter = *overlap_flag() != 0 || p.atomic_gv;
 
   // Gather the corners and form G_c; the lane that staged sample s keeps its G_c
   // in the sample's slot.
   using R = typename Chan<T, CV>::R;
   const bool lane_ok = m.unit_ok && m.t * CV < p.D;
-  const char* img = p.value + int64_t(m.b) * p.S * p.H * p.D * ES;
+  const int64_t img_bytes = int64_t(m.b) * p.S * p.H * p.D * ES;
+  const char* img = p.value + img_bytes;
+  char* gv_img = scatter ? p.grad_value + img_bytes : nullptr;
   const uint32_t lane_bytes = uint32_t(m.t * CV * ES);
   R g{};
   if (lane_ok) g = *reinterpret_cast<const R*>(p.grad_out + (m.gunit * p.D + m.t * CV) * ES);
+  if (gv_img != nullptr && lane_ok) {
+    // Each lane adds weight * grad_out into its channels of every corner with a
+    // non-zero weight, with global atomics (before the dots overwrite the weights).
+    A gw[CV];
+    Chan<T, CV>::from_raw(g, gw);
+    for (int s = 0; s < LP; ++s) {
+      const Staged<A> st = wst[s * m.uw_count + m.uw];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (st.w[c] != A(0)) atomic_add_channels<T, CV>(gv_img + (st.off[c] + lane_bytes), st.w[c], gw);
+    }
+  }
   int s = 0;
   for (; s + kSampleBatch <= LP; s += kSampleBatch)
     corner_dots<T, CV, kSampleBatch>(m, wst, s, lane_ok, img, lane_bytes, g);
@@ -2810,10 +2897,7 @@ int make_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, 
                 (long long)D, (long long)lanes, cv, kWave);
   int lh_log2 = 0;
   while ((1 << lh_log2) < lanes) ++lh_log2;
-  // The forward stages 16-bit weight pairs (StagedPk); the backward stages fp32 / fp64.
-  const size_t staged = (dtype == MSDA_F64)             ? sizeof(Staged<double>)
-                        : (!backward && es == 2 && cv >= 2) ? sizeof(StagedPk)
-                                                            : sizeof(Staged<float>);
+  const size_t staged = dtype == MSDA_F64 ? sizeof(Staged<double>) : sizeof(Staged<float>);
   const size_t levels_bytes = sizeof(Level) * size_t(L);
   // Per wave: the staged records of its units, and the LDS copy of their locations
   // and weights. When one wave's units do not fit, a unit takes more lanes (the
@@ -2903,25 +2987,47 @@ struct BackwardPlan {
   int mfma_nb;            // 16-channel column blocks
   int64_t mfma_blocks;
   size_t mfma_lds;
+  int mfma_table;         // entries of its queue's prefix table
   Plan sample;
 };
 
-size_t device_lds_limit() {
-  int dev = 0, bytes = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
-      bytes <= 0)
-    return 64 * 1024;
-  return size_t(bytes);
+// The attributes the backward plans with, per device: LDS bytes one workgroup may
+// take, and compute units. Read from the runtime on a device's first call and kept
+// (a relaxed atomic per field: concurrent first calls store the same values).
+struct DeviceInfo {
+  std::atomic<int> lds{0}, cus{0};
+};
+constexpr int kMaxDevices = 64;
+DeviceInfo g_devices[kMaxDevices];
+
+void device_info(size_t* lds, int* cus) {
+  int dev = 0;
+  *lds = 64 * 1024;
+  *cus = 256;
+  if (hipGetDevice(&dev) != hipSuccess) return;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int l = g_devices[dev].lds.load(std::memory_order_relaxed);
+    const int c = g_devices[dev].cus.load(std::memory_order_relaxed);
+    if (l > 0 && c > 0) {
+      *lds = size_t(l);
+      *cus = c;
+      return;
+    }
+  }
+  int bytes = 0, n = 0;
+  if (hipDeviceGetAttribute(&bytes, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || bytes <= 0)
+    bytes = 64 * 1024;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+  if (dev >= 0 && dev < kMaxDevices) {
+    g_devices[dev].lds.store(bytes, std::memory_order_relaxed);
+    g_devices[dev].cus.store(n, std::memory_order_relaxed);
+  }
+  *lds = size_t(bytes);
+  *cus = n;
 }
 
-int device_cus() {
-  int dev = 0, n = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-    return 256;
-  return n;
-}
+// Kernel paths a test may force (msda_set_path_override), read once per call.
+std::atomic<int> g_path_override{0};
 
 size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
   const size_t es = size_t(elem_size(dtype));
@@ -2939,7 +3045,7 @@ size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
 int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, int64_t L,
                        int64_t P, int loc_dtype, const void* const* vec_ptrs, int n_vec,
                        const void* grad_attn, size_t lds_limit, int cus, BackwardPlan* plan,
-                       bool accumulate = false) {
+                       bool accumulate = false, int paths = 0) {
   // vec_ptrs: value, grad_output, grad_value (channel vectors), then the locations.
   const int n_chan = std::min(n_vec, 3);
   int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_chan, &plan->sample, elem_size(loc_dtype));
@@ -2989,12 +3095,18 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   const int64_t ls = elem_size(loc_dtype);
   const int64_t per_image = Q * H * std::max(L * P * 2 * ls, D * es);  // 32-bit offsets inside an image
   const bool mfma_sure = 4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc;
+  // The matrix-core kernel's LDS: per wave the staged rows (split for f16 and float)
+  // and the weight tiles, plus its queue's prefix table of (pair, level) entries: at
+  // most 16 x 16 regions per image, an eighth of the (image, region) pairs per queue.
+  const bool mfma_split = dtype != MSDA_BF16;
+  const int mfma_table = int(std::min<int64_t>(kMfmaTable, ((B * 256 + kXcds - 1) / kXcds) * L));
+  const size_t mfma_lds = mfma_lds_bytes(L, D, mfma_split) + sizeof(int) * size_t(2 * mfma_table + 1);
   const bool mfma_likely = 4 * mfma_tiles_estimate + kQueueInts <= bg.keys_alloc && bg.cap >= 64;
   bool mfma_ok = (dtype == MSDA_BF16 || dtype == MSDA_F16 || dtype == MSDA_F32) && D % 16 == 0 &&
                  D / 16 <= kMfmaMaxNb && (mfma_sure || mfma_likely) &&
-                 mfma_lds_bytes(L, D, int(es)) <= lds_limit &&
+                 mfma_lds <= lds_limit &&
                  B * H * mfma_tiles_bound < (int64_t(1) << 31) && per_image < (int64_t(1) << 31) &&
-                 getenv("DEFORMOPS_AMD_NO_MFMA") == nullptr;
+                 !(paths & MSDA_PATH_NO_MFMA);
   for (int i = 0; i < n_chan && mfma_ok; ++i) mfma_ok = aligned(vec_ptrs[i], 16);
   plan->mfma = mfma_ok;
   plan->mfma_fallback = mfma_ok && !mfma_sure;
@@ -3020,12 +3132,13 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   plan->fallback_blocks = xcd_group_grid(H, int64_t(plan->fallback_nw) * B);
   plan->owner_lds = owner_lds_bytes(dtype, L, D, bg.nb, bg.cap);
   plan->mfma_nb = int(D / 16);
-  plan->mfma_lds = mfma_lds_bytes(L, D, int(es));
+  plan->mfma_lds = mfma_lds;
+  plan->mfma_table = mfma_table;
   if (mfma_ok) {
     // Persistent workgroups, as many as fit the CUs at once, a multiple of 8.
-    const int64_t static_lds = sizeof(int) * (2 * kMfmaTable + 1 + kMfmaWaves + 2);
+    const int64_t static_lds = sizeof(int) * (kMfmaWaves + 2 + 3);
     const int64_t per_cu =
-        std::max<int64_t>(1, std::min<int64_t>(mfma_blocks_per_cu(int(D / 16)),
+        std::max<int64_t>(1, std::min<int64_t>(mfma_blocks_per_cu(int(D / 16), es),
                                                int64_t(160 * 1024) / (int64_t(plan->mfma_lds) + static_lds)));
     const int64_t blocks = std::min<int64_t>(B * H * tiles_bound, int64_t(cus) * per_cu);
     plan->mfma_blocks = (blocks + kXcds - 1) / kXcds * kXcds;
@@ -3040,14 +3153,17 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   // Grouped bucketing: groups of 4 samples, LDS counters for every bucket, and the
   // saved keys (16-bit when every key fits) inside grad_value. Not when grad_value's
   // contents are to be accumulated into: the per-sample passes recompute the keys.
+  // The keys of a group are parked as one 8- or 16-byte word, so grad_value must be
+  // aligned to it.
   const void* loc_ptr = n_vec > 3 ? vec_ptrs[3] : nullptr;
-  bg.group4 = !accumulate && (L * P) % 4 == 0 && P % 4 == 0 && plan->bucket &&
-              (loc_ptr == nullptr || aligned(loc_ptr, 16));
+  const void* gv_ptr = n_vec > 2 ? vec_ptrs[2] : nullptr;
   bg.key_bytes = 4 * tiles_bound < 0xffff ? 2 : 4;
+  bg.group4 = !accumulate && (L * P) % 4 == 0 && P % 4 == 0 && plan->bucket &&
+              (loc_ptr == nullptr || aligned(loc_ptr, 16)) && (gv_ptr == nullptr || aligned(gv_ptr, 4 * bg.key_bytes));
   if (B * H * samples_bh * bg.key_bytes > B * S * H * D * es) bg.group4 = 0;
   if (!bg.group4) bg.key_bytes = 0;
   // Per-workgroup counts for the grouped passes, where the device finds them room.
-  bg.chunks = bg.group4 && getenv("DEFORMOPS_AMD_ATOMIC_SORT") == nullptr ? int(plan->bucket_chunks) : 0;
+  bg.chunks = bg.group4 && !(paths & MSDA_PATH_ATOMIC_SORT) ? int(plan->bucket_chunks) : 0;
   plan->scan_blocks = B * H;
   if (bg.chunks > 0)  // a grid-stride loop over (b, h, bucket) when chunked
     plan->scan_blocks = std::max<int64_t>(plan->scan_blocks, std::min<int64_t>((B * H * plan->zero_keys + 255) / 256, 512));
@@ -3111,7 +3227,7 @@ hipError_t launch_owner_mfma(const BackwardPlan& plan, const Problem& p, const i
       const hipError_t e = allow_lds(k, plan.mfma_lds);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(k, dim3(unsigned(plan.mfma_blocks)), dim3(kWave * kMfmaWaves), plan.mfma_lds, st, p,
-                         plan.bg, const_cast<int*>(buckets), entries, accumulate);
+                         plan.bg, const_cast<int*>(buckets), entries, accumulate, plan.mfma_table);
       return hipGetLastError();
     };
     switch (plan.mfma_nb) {
@@ -3244,6 +3360,10 @@ const char* msda_last_error(void) { return g_last_error; }
 
 int msda_abi_version(void) { return MSDA_ABI_VERSION; }
 
+int msda_set_path_override(int paths) {
+  return g_path_override.exchange(paths & (MSDA_PATH_NO_MFMA | MSDA_PATH_ATOMIC_SORT), std::memory_order_relaxed);
+}
+
 int msda_launch_geometry(int value_dtype, int64_t batch, int64_t spatial, int64_t heads,
                          int64_t channels, int64_t queries, int64_t levels, int64_t points,
                          int backward, int* channels_per_lane, int* lanes_per_unit,
@@ -3328,7 +3448,8 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
                   int64_t queries, int64_t levels, int64_t points, int flags, void* stream) {
   g_last_error[0] = '\0';
   int rc = check_call(value_dtype, index_dtype, loc_dtype, batch, spatial, heads, channels,
-                      queries, levels, points, flags, MSDA_SOFTMAX | MSDA_ACCUMULATE_GRAD_VALUE);
+                      queries, levels, points, flags,
+                      MSDA_SOFTMAX | MSDA_ACCUMULATE_GRAD_VALUE | MSDA_GRAD_VALUE_ATOMIC);
   if (rc != MSDA_OK) return rc;
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const int es = elem_size(value_dtype);
@@ -3339,6 +3460,7 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   if (sample_count > 0 && (!grad_sampling_locations || !grad_attention_weights))
     return fail(MSDA_ERR_INVALID, "msda_backward: null location or weight gradient");
   const bool accumulate = flags & MSDA_ACCUMULATE_GRAD_VALUE;
+  const bool atomic_gv = flags & MSDA_GRAD_VALUE_ATOMIC;
   (void)hipGetLastError();
   if (sample_count == 0 || channels == 0 || spatial == 0) {
     // Nothing to sample: grad_value keeps its contents (accumulate) or becomes zero,
@@ -3360,9 +3482,12 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
     return fail(MSDA_ERR_INVALID, "msda_backward: grad_sampling_locations must be 4-byte aligned");
   const void* vec[] = {value, grad_output, grad_value, sampling_locations};
   BackwardPlan plan;
+  size_t lds_limit;
+  int cus;
+  device_info(&lds_limit, &cus);
   rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
-                          loc_dtype, vec, 4, grad_attention_weights, device_lds_limit(), device_cus(),
-                          &plan, accumulate);
+                          loc_dtype, vec, 4, grad_attention_weights, lds_limit, cus, &plan, accumulate,
+                          g_path_override.load(std::memory_order_relaxed));
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,
@@ -3373,6 +3498,11 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   p.grad_value = static_cast<char*>(grad_value);
   p.grad_loc = static_cast<char*>(grad_sampling_locations);
   p.grad_attn = static_cast<char*>(grad_attention_weights);
+  p.atomic_gv = atomic_gv ? 1 : 0;
+  if (atomic_gv && !accumulate) {  // the atomic scatter adds into zeros
+    rc = zero_fill(grad_value, value_bytes, st, "msda_backward");
+    if (rc != MSDA_OK) return rc;
+  }
   // Scratch of the bucket sort: counters in grad_attention_weights, sample indices in
   // grad_sampling_locations; msda_grad_sample_kernel overwrites both last.
   int* buckets = static_cast<int*>(grad_attention_weights);
@@ -3382,7 +3512,8 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
       value_dtype, loc_dtype == MSDA_F32 && value_dtype != MSDA_F32, plan.sample.cv,
       [&]<typename T, typename TL, int CV>() {
         hipError_t e = hipSuccess;
-        if (plan.bucket) {
+        // The atomic scatter needs neither the sort nor the owners.
+        if (plan.bucket && !atomic_gv) {
           e = launch_buckets<TL>(plan, p, buckets, entries, st);
           if (e != hipSuccess) return e;
           if (softmax) {  // per-unit softmax statistics, where the scratch has room
@@ -3395,17 +3526,17 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
             if (e != hipSuccess) return e;
           }
         }
-        if (!accumulate && !plan.mfma) {  // the matrix-core kernel zeroes the gaps itself
+        if (!accumulate && !plan.mfma && !atomic_gv) {  // the matrix-core kernel zeroes the gaps itself
           const int64_t n = int64_t(p.B) * p.S;
           hipLaunchKernelGGL((msda_gap_zero_kernel<T>), dim3(unsigned((n + 255) / 256)), dim3(256),
                              sizeof(Level) * size_t(p.L), st, p);
           e = hipGetLastError();
           if (e != hipSuccess) return e;
         }
-        if (plan.mfma)
+        if (plan.mfma && !atomic_gv)
           e = softmax ? launch_owner_mfma<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
                       : launch_owner_mfma<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
-        if (e == hipSuccess && (!plan.mfma || plan.mfma_fallback)) {
+        if (e == hipSuccess && !atomic_gv && (!plan.mfma || plan.mfma_fallback)) {
           const int after_mfma = plan.mfma ? 1 : 0;
           e = softmax ? launch_owner_cvr<T, TL, true>(plan, p, buckets, entries, int(accumulate), after_mfma, st)
                       : launch_owner_cvr<T, TL, false>(plan, p, buckets, entries, int(accumulate), after_mfma, st);

@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MSDA_ABI_VERSION 1
+#define MSDA_ABI_VERSION 2
 
 /* Element types. value and attention_weights share one; locations may be
  * MSDA_F32 or the value type (MSDA_F64 only with MSDA_F64 values). */
@@ -54,6 +54,13 @@ enum msda_index_dtype {
 enum msda_flags {
   MSDA_SOFTMAX = 1,               /* normalize attention_weights over the L * P points */
   MSDA_ACCUMULATE_GRAD_VALUE = 2, /* backward: add into grad_value instead of overwriting it */
+  MSDA_GRAD_VALUE_ATOMIC = 4,     /* backward: grad_value by global atomics (see msda_backward) */
+};
+
+/* Kernel paths msda_set_path_override can force. */
+enum msda_path_bits {
+  MSDA_PATH_NO_MFMA = 1,     /* grad_value on the VALU owner kernel instead of the matrix cores */
+  MSDA_PATH_ATOMIC_SORT = 2, /* bucket sort publishing counts with global atomics */
 };
 
 /* Return codes. */
@@ -97,10 +104,24 @@ int msda_forward(const void* value, int value_dtype,
  * contributions in fp32 (fp64 for MSDA_F64) and stores once; with
  * MSDA_ACCUMULATE_GRAD_VALUE the previous contents are added to that sum. No
  * atomics touch grad_value, it needs no zero-fill, and there is no float32 copy.
+ * For bf16, f16 and float values the owner sums on the matrix cores with each
+ * weight * grad_out product formed from 16-bit-significand parts (relative error
+ * at most 2^-16 for bf16, 2^-15 for f16, 3 * 2^-16 for float; see msda.hip).
  * The order in which an element's contributions are summed follows the order the
  * bucket sort gives the samples, which depends on the order of its LDS atomics
  * across waves; so the last bits of grad_value may vary between runs. The other two
- * gradients are written in full, zeros included. While the call
+ * gradients are written in full, zeros included.
+ *
+ * With MSDA_GRAD_VALUE_ATOMIC, or when two valid levels of the table share
+ * positions of S (found on the device), grad_value is instead zero-filled (unless
+ * MSDA_ACCUMULATE_GRAD_VALUE) and every sample adds weight * grad_out into its
+ * corners with global atomics in the value dtype (fp32 / fp64 adds, packed bf16 /
+ * f16 pair adds), the mechanism of the reference's kernels
+ * (include/interpolate.cuh:146-175, and the native-dtype atomics of the Triton
+ * zero-buffer backward, backends/triton/_kernels/msda_query_tiled.py:435-483).
+ * Overlapping levels then sum their contributions into a shared element, as the
+ * reference's eager and atomic paths do. A 16-bit grad_value accumulates in its own
+ * dtype there, so it carries one rounding per contribution. While the call
  * runs, its outputs serve as its scratch (a bucket sort of the samples by pyramid
  * tile): grad_sampling_locations holds the sorted sample indices,
  * grad_attention_weights the bucket counters, and grad_value the samples' keys
@@ -133,6 +154,13 @@ const char* msda_last_error(void);
 
 /* MSDA_ABI_VERSION of the loaded library. */
 int msda_abi_version(void);
+
+/* Forces kernel paths of later calls in this process (msda_path_bits; 0 restores
+ * the library's own choice) and returns the previous bits. No counterpart in the
+ * reference: it lets a test run every grad_value and sort path the library has on
+ * inputs where another path would be chosen. Results are the same on every path
+ * up to rounding. Not meant to be changed while calls run on other threads. */
+int msda_set_path_override(int paths);
 
 /* The launch layout msda_forward / msda_backward would use for these sizes:
  * channels per lane, lanes per (query, head) unit and waves per workgroup. Host

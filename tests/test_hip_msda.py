@@ -171,28 +171,24 @@ def test_wider_shapes_at_encoder_size(device, sizes, dtype):
 
 # The two grad_value kernels for float and 16-bit dtypes: the matrix-core one (the
 # default for D = 16, 32, 48, 64) and the VALU owner kernel (every other case, float64,
-# and the fallback when the bucket scratch is short), selected by
-# DEFORMOPS_AMD_NO_MFMA; and the two
-# ways the bucket sort publishes its counts: per-workgroup count rows (the default
-# where the scratch has room) or global atomics, forced by DEFORMOPS_AMD_ATOMIC_SORT.
+# and the fallback when the bucket scratch is short), forced by PATH_NO_MFMA; and the
+# two ways the bucket sort publishes its counts: per-workgroup count rows (the default
+# where the scratch has room) or global atomics, forced by PATH_ATOMIC_SORT.
+
+PATH_BITS = {"mfma": 0, "mfma-atomic-sort": 2, "valu": 1, "valu-atomic-sort": 3}
 
 
-@pytest.mark.parametrize("path", ["mfma", "mfma-atomic-sort", "valu", "valu-atomic-sort"])
+@pytest.mark.parametrize("path", sorted(PATH_BITS))
 @pytest.mark.parametrize("dtype", [BF16, F16, F32], ids=["bf16", "f16", "f32"])
 @pytest.mark.parametrize("cfg", [2, 3])
-def test_grad_value_paths_match_oracle(device, monkeypatch, cfg, dtype, path):
-    if path.startswith("valu"):
-        monkeypatch.setenv("DEFORMOPS_AMD_NO_MFMA", "1")
-    else:
-        monkeypatch.delenv("DEFORMOPS_AMD_NO_MFMA", raising=False)
-    if path.endswith("atomic-sort"):
-        monkeypatch.setenv("DEFORMOPS_AMD_ATOMIC_SORT", "1")
-    else:
-        monkeypatch.delenv("DEFORMOPS_AMD_ATOMIC_SORT", raising=False)
+def test_grad_value_paths_match_oracle(device, cfg, dtype, path):
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
     w = make_workload(cfg).to(device, dtype)
-    for softmax in (False, True):
-        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
-                             label=f"config {cfg} {path}")
+    with _lib.path_override(PATH_BITS[path]):
+        for softmax in (False, True):
+            check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                                 label=f"config {cfg} {path}")
 
 
 @pytest.mark.parametrize(("dtype", "queries"), [(BF16, 256), (F32, 128)], ids=["bf16", "f32"])
@@ -248,6 +244,156 @@ def test_accumulate_flag_adds_into_grad_value(device, dtype, cfg, sizes, softmax
     assert rel_err(added[0], expected.cpu()) <= BWD_TOL[dtype]
     torch.testing.assert_close(added[1], plain[1], rtol=0, atol=0)
     torch.testing.assert_close(added[2], plain[2], rtol=0, atol=0)
+
+
+def abi_backward(w, flags, *, softmax=False, grad_value=None):
+    """One backward C-ABI call on a workload; returns (grad_value, grad_loc, grad_attn)."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    lib = _lib.load()
+    value, shapes, starts, loc, attn = w.operands(softmax=softmax)
+    B, S, H, D, Q, L, P = w.sizes
+    gv = torch.empty_like(value) if grad_value is None else grad_value
+    gl, ga = torch.empty_like(loc), torch.empty_like(attn)
+    flags |= _lib.FLAG_SOFTMAX if softmax else 0
+    lib.check(lib.backward(value.data_ptr(), _lib.DTYPE_CODES[value.dtype], shapes.data_ptr(), starts.data_ptr(),
+                           _lib.INDEX_CODES[shapes.dtype], loc.data_ptr(), _lib.DTYPE_CODES[loc.dtype],
+                           attn.data_ptr(), w.grad_output.data_ptr(), gv.data_ptr(), gl.data_ptr(), ga.data_ptr(),
+                           B, S, H, D, Q, L, P, flags, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    return gv, gl, ga
+
+
+@pytest.mark.parametrize("softmax", [False, True], ids=["linear", "softmax"])
+@pytest.mark.parametrize(
+    ("dtype", "sizes"),
+    [
+        pytest.param(F32, {}, id="f32"),
+        pytest.param(F64, {}, id="f64"),
+        pytest.param(BF16, {"queries": 100}, id="bf16"),
+        pytest.param(F16, {"queries": 100}, id="f16"),
+        pytest.param(BF16, {"queries": 100, "channels": 7}, id="bf16-one-channel-per-lane"),
+        pytest.param(F16, {"queries": 100, "channels": 9, "heads": 3}, id="f16-one-channel-per-lane"),
+    ],
+)
+def test_atomic_grad_value_flag_matches_oracle(device, dtype, sizes, softmax):
+    """MSDA_GRAD_VALUE_ATOMIC: grad_value zero-filled, then scattered with global
+    atomics in the value dtype (the reference's mechanism, include/interpolate.cuh:
+    146-175). grad_value matches the oracle; the other two gradients are bit-equal to
+    the default path's. 16-bit grad_value sums in its own dtype (one rounding per
+    contribution), so those cases keep the coarsest level's fan-in near 100."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    w = make_workload(0, **sizes).to(device, dtype)
+    value, shapes, starts, loc, attn = w.operands(softmax=softmax)
+    atomic = abi_backward(w, _lib.FLAG_GRAD_VALUE_ATOMIC, softmax=softmax)
+    owner = abi_backward(w, 0, softmax=softmax)
+    expected = oracle.backward(value, shapes, starts, loc, attn, w.grad_output, softmax=softmax)[0]
+    assert rel_err(atomic[0], expected) <= BWD_TOL[dtype]
+    torch.testing.assert_close(atomic[1], owner[1], rtol=0, atol=0)
+    torch.testing.assert_close(atomic[2], owner[2], rtol=0, atol=0)
+    previous = torch.randn(value.shape, generator=torch.Generator().manual_seed(5)).to(device, dtype)
+    added = abi_backward(w, _lib.FLAG_GRAD_VALUE_ATOMIC | _lib.FLAG_ACCUMULATE_GRAD_VALUE, softmax=softmax,
+                         grad_value=previous.clone())[0]
+    assert rel_err(added, (previous.double().cpu() + expected)) <= BWD_TOL[dtype]
+
+
+@pytest.mark.parametrize("path", ["mfma", "valu"])
+@pytest.mark.parametrize("dtype", [BF16, F16], ids=["bf16", "f16"])
+def test_weights_keep_fp32_precision(device, dtype, path):
+    """The attention * bilinear weights stay fp32 in 16-bit calls, as in the reference
+    (the fp32 acc of its Triton and CUDA kernels). Two queries sample the same two places
+    (left, where value is +1, and right, where it is -1) at dx = 5/16, dy = 3/16 with
+    attention weights a0 = 91/128 and a1 = 181/256 swapped between them, and grad_out
+    is +1 for query 0 and -1 for query 1. Every product a * bilinear has 15
+    significant bits, so rounding it to 16 bits (8 significant bits for bf16) would
+    move the results by ~2^-9 a; the exact results are tiny by cancellation:
+      output[q0] = a0 - a1 = 2^-8, output[q1] = -2^-8,
+      grad_value = +-bilinear_c * 2^-8 at the corners of the left / right sample.
+    All are representable, so fp32 weights give them exactly."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    W = Hh = 16
+    D = 16
+    value = torch.ones(1, Hh, W, 1, D, dtype=F64)
+    value[:, :, W // 2:] = -1.0
+    value = value.reshape(1, Hh * W, 1, D)
+    x_left, x_right, y = 3 + 5 / 16, 11 + 5 / 16, 5 + 3 / 16
+    # Queries past the first two have zero weight and gradient; they only give the
+    # backward's sort enough scratch for the matrix-core kernel's counters.
+    Q = 512
+    loc = torch.tensor([(x_left + 0.5) / W, (y + 0.5) / Hh, (x_right + 0.5) / W, (y + 0.5) / Hh], dtype=F64)
+    loc = loc.view(1, 1, 1, 1, 2, 2).expand(1, Q, 1, 1, 2, 2).contiguous()
+    a0, a1 = 91 / 128, 181 / 256
+    attn = torch.zeros(1, Q, 1, 2, dtype=F64)
+    attn[0, :2, 0] = torch.tensor([[a0, a1], [a1, a0]], dtype=F64)
+    grad_out = torch.zeros(1, Q, D, dtype=F64)
+    grad_out[0, 0], grad_out[0, 1] = 1.0, -1.0
+    shapes = torch.tensor([[Hh, W]])
+    starts = torch.tensor([0])
+    ops = [t.to(device, dtype) for t in (value, loc, attn, grad_out)]
+    for t, ref in zip(ops, (value, loc, attn, grad_out)):
+        assert torch.equal(t.double().cpu(), ref)  # the inputs are exact in the dtype
+    with _lib.path_override(1 if path == "valu" else 0):
+        out, gv, _, _ = run_hip(ops[0], shapes.to(device), starts.to(device), ops[1], ops[2], ops[3],
+                                softmax=False)
+    expected_out = oracle.forward(value, shapes, starts, loc, attn, softmax=False)
+    expected_gv = oracle.backward(value, shapes, starts, loc, attn, grad_out, softmax=False)[0]
+    assert expected_out.abs().max().item() == 2.0**-8
+    torch.testing.assert_close(out.double().cpu(), expected_out.reshape(out.shape), rtol=0, atol=0)
+    torch.testing.assert_close(gv.double().cpu(), expected_gv.reshape(gv.shape), rtol=0, atol=0)
+
+
+@pytest.mark.parametrize(("cfg", "dtype"), [(2, BF16), (2, F16), (3, BF16), (4, BF16), (4, F16)])
+def test_sixteen_bit_error_margin(device, cfg, dtype):
+    """The measured norm-wise errors of 16-bit calls at configs 2-4 (config 4 at one
+    image), printed, against a bound of two roundings to the value dtype (2^-8 for
+    bf16, 2^-10 for f16): the result is one fp32 computation rounded once to the
+    dtype, so it sits far inside the 2e-2 tolerance of the north star."""
+    sizes = {"batch": 1} if cfg == 4 else {}
+    w = make_workload(cfg, **sizes).to(device, dtype)
+    bound = 2.0**-8 if dtype == BF16 else 2.0**-10
+    for softmax in (False, True):
+        errs = check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                                    label=f"config {cfg}")
+        print(f"config {cfg} {dtype} softmax={softmax}: {errs}")
+        assert max(errs.values()) <= bound, errs
+
+
+# Overlapping level tables: two valid levels that share positions of S. The forward
+# samples each level as given; the backward sums every level's contribution into a
+# shared grad_value element, as the oracle and the reference's eager path do (its
+# flat indices start + y W + x, backends/eager/msda_pytorch.py:83-112, under autograd).
+OVERLAPS = [
+    # (levels, starts, S): level 1 starts inside level 0
+    pytest.param(((6, 5), (4, 4)), (0, 10), 30, id="second-inside-first"),
+    # identical levels, both at 0
+    pytest.param(((5, 5), (5, 5)), (0, 0), 25, id="same-level-twice"),
+    # three levels, the last overlapping the first two
+    pytest.param(((8, 8), (4, 4), (6, 6)), (0, 64, 50), 86, id="third-spans-two"),
+]
+
+
+@pytest.mark.parametrize("path", ["default", "valu"])
+@pytest.mark.parametrize("dtype", [F32, BF16, F64], ids=["f32", "bf16", "f64"])
+@pytest.mark.parametrize(("levels", "starts", "S"), OVERLAPS)
+def test_overlapping_levels_sum_into_grad_value(device, levels, starts, S, dtype, path):
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    L = len(levels)
+    g = torch.Generator().manual_seed(17)
+    B, Q, H, D, P = 2, 30, 2, 16, 4
+    value = torch.randn(B, S, H, D, generator=g, dtype=F64)
+    loc = torch.rand(B, Q, H, L, P, 2, generator=g, dtype=F64) * 1.1 - 0.05
+    attn = torch.softmax(torch.randn(B, Q, H, L * P, generator=g, dtype=F64), -1)
+    grad_out = torch.randn(B, Q, H * D, generator=g, dtype=F64)
+    shapes = torch.tensor(levels, dtype=torch.int64)
+    start_t = torch.tensor(starts, dtype=torch.int64)
+    ops = [t.to(device, dtype) for t in (value, loc, attn, grad_out)]
+    with _lib.path_override(1 if path == "valu" else 0):
+        for softmax in (False, True):
+            check_against_oracle(ops[0], shapes.to(device), start_t.to(device), ops[1], ops[2], ops[3],
+                                 softmax=softmax, dtype=dtype, label=f"overlap {levels} {starts} {path}")
 
 
 @pytest.mark.parametrize("dtype", [BF16, F32], ids=["bf16", "f32"])

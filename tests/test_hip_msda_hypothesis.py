@@ -7,13 +7,11 @@ width (odd ones included), levels and their shapes, points, queries, value dtype
 gradients against the float64 C oracle with the tolerances of
 ``tests/test_hip_msda.py``. The owner kernel for grad_value (matrix cores or VALU)
 and the bucket sort's counting mode (per-workgroup rows or atomics) are drawn too,
-through the library's environment switches. Examples are derandomized, so a GPU run
+through the library's path override (msda_set_path_override). Examples are derandomized, so a GPU run
 replays the same cases.
 """
 
 from __future__ import annotations
-
-import os
 
 import pytest
 import torch
@@ -25,12 +23,8 @@ from tests.workloads import make_workload
 
 pytestmark = pytest.mark.gpu
 
-PATHS = {
-    "default": {},
-    "valu": {"DEFORMOPS_AMD_NO_MFMA": "1"},
-    "atomic-sort": {"DEFORMOPS_AMD_ATOMIC_SORT": "1"},
-    "valu-atomic-sort": {"DEFORMOPS_AMD_NO_MFMA": "1", "DEFORMOPS_AMD_ATOMIC_SORT": "1"},
-}
+#: Kernel paths (msda_set_path_override bits): VALU owner kernel, atomic sort.
+PATHS = {"default": 0, "valu": 1, "atomic-sort": 2, "valu-atomic-sort": 3}
 
 
 @st.composite
@@ -58,21 +52,14 @@ def cases(draw):
           suppress_health_check=[HealthCheck.too_slow, HealthCheck.data_too_large,
                                  HealthCheck.function_scoped_fixture])
 def test_random_shapes_match_oracle(device, case):
-    env = PATHS[case["path"]]
-    saved = {k: os.environ.get(k) for k in env}
-    os.environ.update(env)
-    try:
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    with _lib.path_override(PATHS[case["path"]]):
         w = make_workload(0, levels=case["levels"], batch=case["batch"], queries=case["queries"],
                           heads=case["heads"], channels=case["channels"], points=case["points"],
                           seed=case["seed"]).to(device, case["dtype"])
         check_against_oracle(*w.operands(softmax=case["softmax"]), w.grad_output, softmax=case["softmax"],
                              dtype=case["dtype"], label=str(case))
-    finally:
-        for k, v in saved.items():
-            if v is None:
-                os.environ.pop(k, None)
-            else:
-                os.environ[k] = v
 
 
 @st.composite
