@@ -5,27 +5,35 @@ config 4 (Mask2Former pixel-decoder encoder, large): B=4, levels 128x128, 64x64,
 32x32 (Q = S = 21,504), H=8, D=32, P=4, bfloat16 value, weights and locations,
 linear method, synthetic seeded inputs already resident in HBM.
 
-Prints one JSON line: ``value`` is fwd+bwd milliseconds per call (lower is
-better); ``roofline`` rates the dominant launch, the backward C-ABI call (its
-kernels run back to back on one stream), by its algorithmic bytes over its average
-duration, timed with HIP events on that stream; ``cpu_baseline`` times the torch
+Prints one JSON line. ``value`` is fwd+bwd milliseconds per call through the
+public API (lower is better). ``roofline`` rates one fwd+bwd pair of C-ABI calls
+(the forward kernel, then the backward's kernels, back to back on one stream,
+bracketed by HIP events on that stream) by its algorithmic bytes against 8 TB/s;
+``roofline.backward_call`` rates the backward call alone, and ``roofline.gather``
+rates the forward kernel's corner gathers against the random-row gather rate of
+L1 and L2 that the row-gather probe (libmsda_probe.so) measures in the same run.
+``roofline.traffic`` is the HBM bytes of one fwd+bwd from the rocprofv3 counter
+passes in profiles/msda_config4_bf16_hbm_traffic.md, reported only when those
+passes ran on the kernel source being measured. ``cpu_baseline`` times the torch
 restatement of the reference's eager CPU path on a bounded sample of the same
-workload, scaled to one full call.
+workload, scaled to one full call, on all physical cores.
 
     python bench.py [--steps K] [--warmup W] [--dtype bf16|f16|f32] [--loc-dtype ...]
-                    [--method linear|softmax] [--config 0..4]
+                    [--method linear|softmax] [--config 0..4] [--grad-value owner|atomic]
 
-``--config`` measures another BASELINE configuration the same way (config 4, the
-headline, is the default and the only one the driver's line is quoted on). The
-``roofline.traffic`` figure is the profiled one of config 4 (bf16, linear) and is
-null for every other workload.
+``--config`` measures another BASELINE configuration the same way (config 4 is the
+headline and the only one the driver's line is quoted on). ``--grad-value atomic``
+runs the backward's grad_value with global atomics (MSDA_GRAD_VALUE_ATOMIC) in the
+C-ABI timings, for comparison with the owner-computes default.
 """
 
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -40,12 +48,9 @@ from tests.workloads import CONFIGS, algorithmic_bytes, make_workload  # noqa: E
 
 METRIC = "MSDA fwd+bwd ms/call + achieved HBM GB/s, 21.5k-query bf16 encoder, 1 GPU"
 PEAK_HBM_GBS = 8000.0
-# HBM bytes of one backward C-ABI call on the default workload (bf16 value, weights
-# and locations, linear method): rocprofv3 FETCH_SIZE x 2 + WRITE_SIZE x 1, summed
-# over the call's kernels, each counter scaled by what it reads for a 256 MiB copy.
-# profiles/msda_config4_bf16_hbm_traffic.md holds the passes and the calibration.
-BACKWARD_TRAFFIC_BYTES = 1_129_519_424
 DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+KERNEL_SOURCE = REPO / "deformops_amd" / "csrc" / "msda.hip"
+TRAFFIC_PROFILE = REPO / "profiles" / "msda_config4_bf16_hbm_traffic.md"
 
 
 def _events(n: int) -> list[torch.cuda.Event]:
@@ -53,7 +58,7 @@ def _events(n: int) -> list[torch.cuda.Event]:
 
 
 def time_fwd_bwd(w, steps: int, warmup: int, softmax: bool):
-    """Time K full fwd+bwd steps through the public API; per-step events + wall clock."""
+    """Time K full fwd+bwd steps through the public API; wall clock and per-step events."""
     from deformops_amd.registry import msda  # noqa: PLC0415
 
     value, shapes, starts, loc, attn = w.operands(softmax=softmax)
@@ -81,24 +86,17 @@ def time_fwd_bwd(w, steps: int, warmup: int, softmax: bool):
     return wall_ms / steps, statistics.median(per_step)
 
 
-def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
-    """Average device time of each direction alone, through the C ABI, on torch's stream.
-
-    The forward is one kernel. The backward call launches the bucket sort of the
-    samples (clear, count, scan, place), the per-unit softmax statistics (softmax
-    only), the owner-computes grad_value kernel (which also zeroes positions no level
-    covers) and the location / weight gradient kernel, all on this stream; the events
-    bracket the whole call.
-    """
+def time_calls(w, steps: int, warmup: int, softmax: bool, bwd_flags: int) -> dict[str, float]:
+    """Average device time of the C-ABI calls on torch's current stream: the forward
+    (one kernel), the backward (the bucket sort, the softmax statistics, grad_value,
+    grad_sample), and a forward then a backward back to back."""
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
 
     lib = _lib.load()
     value, shapes, starts, loc, attn = w.operands(softmax=softmax)
     B, S, H, D, Q, L, P = w.sizes
     out = torch.empty((B, Q, H * D), dtype=value.dtype, device=value.device)
-    gv = torch.empty_like(value)
-    gl = torch.empty_like(loc)
-    ga = torch.empty_like(attn)
+    gv, gl, ga = torch.empty_like(value), torch.empty_like(loc), torch.empty_like(attn)
     stream = torch.cuda.current_stream()
     flags = _lib.FLAG_SOFTMAX if softmax else 0
     vcode, lcode = _lib.DTYPE_CODES[value.dtype], _lib.DTYPE_CODES[loc.dtype]
@@ -113,60 +111,159 @@ def time_kernels(w, steps: int, warmup: int, softmax: bool) -> dict[str, float]:
         lib.check(lib.backward(value.data_ptr(), vcode, shapes.data_ptr(), starts.data_ptr(), icode,
                                loc.data_ptr(), lcode, attn.data_ptr(), w.grad_output.data_ptr(),
                                gv.data_ptr(), gl.data_ptr(), ga.data_ptr(),
-                               B, S, H, D, Q, L, P, flags, stream.cuda_stream))
+                               B, S, H, D, Q, L, P, flags | bwd_flags, stream.cuda_stream))
+
+    def both() -> None:
+        fwd()
+        bwd()
 
     result = {}
-    for name, fn in (("forward", fwd), ("backward", bwd)):
+    for name, fn in (("forward", fwd), ("backward", bwd), ("fwd_bwd", both)):
         for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
-        times = []
+        marks = []
         for _ in range(steps):
             s, e = _events(2)
             s.record(stream)
             fn()
             e.record(stream)
-            times.append((s, e))
+            marks.append((s, e))
         torch.cuda.synchronize()
-        result[name] = statistics.mean(s.elapsed_time(e) for s, e in times)
+        result[name] = statistics.mean(s.elapsed_time(e) for s, e in marks)
     return result
 
 
+def row_gather_rates(device: torch.device) -> dict[str, float]:
+    """GB/s of random 64-byte row gathers (4 lanes x 16 bytes each) from a 16 KiB buffer
+    (L1-resident on every CU) and a 2 MiB one (L2-resident on every XCD), from the
+    probe kernel of libmsda_probe.so; mean of 5 launches of 2048 x 256 threads."""
+    import ctypes  # noqa: PLC0415
+
+    path = REPO / "deformops_amd" / "lib" / "libmsda_probe.so"
+    probe = ctypes.CDLL(str(path))
+    probe.msda_probe_row_gather.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_void_p, ctypes.c_void_p]
+    probe.msda_probe_row_gather.restype = ctypes.c_int
+    blocks, iters, threads = 2048, 128, 256
+    sink = torch.empty(blocks * threads, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream()
+    rates = {}
+    for name, nbytes in (("l1", 16 << 10), ("l2", 2 << 20)):
+        buf = torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device=device)
+        rows = nbytes // 64
+
+        def launch() -> None:
+            rc = probe.msda_probe_row_gather(buf.data_ptr(), rows, blocks, iters, sink.data_ptr(),
+                                             stream.cuda_stream)
+            if rc != 0:
+                raise RuntimeError("row-gather probe launch failed")
+
+        for _ in range(2):
+            launch()
+        times = []
+        for _ in range(5):
+            s, e = _events(2)
+            s.record(stream)
+            launch()
+            e.record(stream)
+            e.synchronize()
+            times.append(s.elapsed_time(e))
+        gathered = blocks * (threads // 64) * 16 * iters * 8 * 64  # waves x groups x rows x bytes
+        rates[name] = gathered / (statistics.mean(times) * 1e-3) / 1e9
+    return rates
+
+
+def profiled_traffic() -> tuple[int | None, str]:
+    """HBM bytes of one fwd+bwd of the default workload, from the counter passes in
+    profiles/, when they ran on this kernel source; else ``None`` and why."""
+    if not TRAFFIC_PROFILE.exists():
+        return None, "no counter profile committed"
+    text = TRAFFIC_PROFILE.read_text()
+    sha = re.search(r"kernel_source_sha256:\s*([0-9a-f]{64})", text)
+    total = re.search(r"traffic_bytes_per_fwd_bwd:\s*(\d+)", text)
+    if not sha or not total:
+        return None, "the counter profile states no source hash or total"
+    current = hashlib.sha256(KERNEL_SOURCE.read_bytes()).hexdigest()
+    if sha.group(1) != current:
+        return None, "the counter profile was taken on another kernel source"
+    return int(total.group(1)), f"rocprofv3 FETCH_SIZE x2 + WRITE_SIZE passes, {TRAFFIC_PROFILE.relative_to(REPO)}"
+
+
+def host_cpu() -> dict:
+    """The host's CPU model, logical CPUs and physical cores (from /proc/cpuinfo)."""
+    model, cores = "unknown", set()
+    try:
+        phys = core = None
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            key, _, val = (part.strip() for part in line.partition(":"))
+            if key == "model name":
+                model = val
+            elif key == "physical id":
+                phys = val
+            elif key == "core id":
+                core = val
+            elif not line.strip() and core is not None:
+                cores.add((phys, core))
+                phys = core = None
+    except OSError:
+        pass
+    logical = os.cpu_count() or 1
+    return {"model": model, "logical_cpus": logical, "physical_cores": len(cores) or logical}
+
+
 def cpu_baseline(config: int, dtype: torch.dtype, loc_dtype: torch.dtype, softmax: bool) -> dict:
-    """The reference's eager CPU path (torch restatement) on a bounded sample.
+    """The reference's eager CPU path (torch restatement) on a bounded sample, on all
+    physical cores: in the workload's dtype, and in float32 too when that differs
+    (the CPU accumulates 16-bit dtypes in 16 bits).
 
     Sample: batch 1 and at most the first 21,504 queries of the configuration (at
-    config 4, one image: 21,504 of the 86,016 (batch, query) pairs), same dtype;
-    1 warm-up and 3 timed fwd + autograd-bwd iterations, median, scaled by the
-    call's (batch, query) pairs over the sample's.
+    config 4, one image: 21,504 of the 86,016 (batch, query) pairs); 1 warm-up and 3
+    timed fwd + autograd-bwd iterations, median, scaled by the call's (batch, query)
+    pairs over the sample's.
     """
     from oracle.eager import eager_msda  # noqa: PLC0415
 
+    cpu = host_cpu()
+    threads_before = torch.get_num_threads()
+    torch.set_num_threads(cpu["physical_cores"])
     cfg = CONFIGS[config]
-    queries = make_workload(cfg, batch=1).sizes[4]
-    sample_queries = min(queries, 21504)
-    w = make_workload(cfg, batch=1, queries=sample_queries).to("cpu", dtype, loc_dtype)
-    value, shapes, starts, loc, attn = w.operands(softmax=softmax)
-    times = []
-    for i in range(4):
-        leaves = [t.detach().clone().requires_grad_(True) for t in (value, loc, attn)]
-        t0 = time.perf_counter()
-        out = eager_msda(leaves[0], shapes, starts, leaves[1], leaves[2], softmax=softmax)
-        out.backward(w.grad_output)
-        if i:
-            times.append(time.perf_counter() - t0)
-    full_pairs = cfg.batch * queries
-    scale = full_pairs / (1 * sample_queries)
+    full_queries = cfg.queries if cfg.queries is not None else sum(h * w for h, w in cfg.levels)
+    sample_queries = min(full_queries, 21504)
+    base = make_workload(cfg, batch=1, queries=sample_queries)
+
+    def median_ms(dt: torch.dtype, lt: torch.dtype) -> float:
+        w = base.to("cpu", dt, lt)
+        value, shapes, starts, loc, attn = w.operands(softmax=softmax)
+        times = []
+        for i in range(4):
+            leaves = [t.detach().clone().requires_grad_(True) for t in (value, loc, attn)]
+            t0 = time.perf_counter()
+            out = eager_msda(leaves[0], shapes, starts, leaves[1], leaves[2], softmax=softmax)
+            out.backward(w.grad_output)
+            if i:
+                times.append(time.perf_counter() - t0)
+        return statistics.median(times) * 1e3
+
+    scale = cfg.batch * full_queries / sample_queries
+    try:
+        value_ms = median_ms(dtype, loc_dtype) * scale
+        f32_ms = value_ms if dtype == torch.float32 else median_ms(torch.float32, torch.float32) * scale
+    finally:
+        torch.set_num_threads(threads_before)
+    name = str(dtype).split(".")[-1]
     return {
-        "value": statistics.median(times) * 1e3 * scale,
+        "value": round(value_ms, 2),
         "unit": "ms/call",
-        "cores": torch.get_num_threads(),
+        "cores": cpu["physical_cores"],
         "kind": "port",
+        "value_float32": round(f32_ms, 2),
+        "cpu": cpu,
         "sample": (
             f"torch restatement of the reference eager backend (backends/eager/msda_pytorch.py) "
-            f"fwd + autograd bwd, {str(dtype).split('.')[-1]}, batch 1 x {sample_queries} queries "
+            f"fwd + autograd bwd, {name} (and float32 for value_float32), batch 1 x {sample_queries} queries "
             f"of config {config} (1/{scale:g} of a call), median of 3 after 1 warm-up, scaled x{scale:g}; "
-            f"host {os.cpu_count()} logical CPUs"
+            f"torch.set_num_threads({cpu['physical_cores']}) on {cpu['model']}"
         ),
     }
 
@@ -180,6 +277,7 @@ def main() -> int:
     parser.add_argument("--loc-dtype", choices=sorted(DTYPES), default=None)
     parser.add_argument("--method", choices=["linear", "softmax"], default="linear")
     parser.add_argument("--config", type=int, choices=sorted(CONFIGS), default=4)
+    parser.add_argument("--grad-value", choices=["owner", "atomic"], default="owner")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument(
         "--copy-calibration", type=int, default=0, metavar="MIB",
@@ -213,19 +311,29 @@ def main() -> int:
             torch.mul(src, 1.0, out=dst)  # one elementwise kernel: reads and writes MIB MiB
         torch.cuda.synchronize()
         del src, dst
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
     cfg = CONFIGS[args.config]
     w = make_workload(cfg).to(device, dtype, loc_dtype)
     B, S, H, D, Q, L, P = w.sizes
     es = torch.empty((), dtype=dtype).element_size()
     ls = torch.empty((), dtype=loc_dtype).element_size()
     fwd_bytes, bwd_bytes = algorithmic_bytes(B, S, H, D, Q, L, P, es, ls)
+    bwd_flags = _lib.FLAG_GRAD_VALUE_ATOMIC if args.grad_value == "atomic" else 0
 
+    calls = time_calls(w, args.steps, args.warmup, softmax, bwd_flags)
+    gather = row_gather_rates(device)
     ms_per_step, median_ms = time_fwd_bwd(w, args.steps, args.warmup, softmax)
-    kernels = time_kernels(w, args.steps, args.warmup, softmax)
-    bwd_gbs = bwd_bytes / (kernels["backward"] * 1e-3) / 1e9
-    total_gbs = (fwd_bytes + bwd_bytes) / (ms_per_step * 1e-3) / 1e9
 
-    profiled = args.config == 4 and args.dtype == "bf16" and loc_dtype == torch.bfloat16 and not softmax
+    total_gbs = (fwd_bytes + bwd_bytes) / (ms_per_step * 1e-3) / 1e9
+    call_gbs = (fwd_bytes + bwd_bytes) / (calls["fwd_bwd"] * 1e-3) / 1e9
+    bwd_gbs = bwd_bytes / (calls["backward"] * 1e-3) / 1e9
+    corner_bytes = B * Q * H * L * P * 4 * D * es  # every sample loads 4 corner rows
+    corner_gbs = corner_bytes / (calls["forward"] * 1e-3) / 1e9
+    default = args.config == 4 and args.dtype == "bf16" and loc_dtype == torch.bfloat16 and not softmax
+    traffic, traffic_source = profiled_traffic() if default and args.grad_value == "owner" else (
+        None, "profiled for the default workload only")
+
     levels = "/".join(f"{h}x{w_}" for h, w_ in cfg.levels)
     queries = f"Q=S={S}" if cfg.queries is None else f"Q={Q}, S={S}"
     line = {
@@ -247,24 +355,45 @@ def main() -> int:
                 f"P={P}, {args.dtype} value/weights, {str(loc_dtype).split('.')[-1]} locations, "
                 f"{args.method} method, fwd+bwd via deformops_amd.registry.msda"
             ),
+            "grad_value": args.grad_value,
             "fwd_bwd_bytes": fwd_bytes + bwd_bytes,
             "fwd_bwd_achieved_gb_s": round(total_gbs, 1),
             "fwd_bwd_frac_of_hbm_peak": round(total_gbs / PEAK_HBM_GBS, 4),
             "median_ms_per_step": round(median_ms, 5),
-            "forward_kernel_ms": round(kernels["forward"], 5),
-            "backward_kernel_ms": round(kernels["backward"], 5),
-            "forward_kernel_gb_s": round(fwd_bytes / (kernels["forward"] * 1e-3) / 1e9, 1),
+            "forward_call_ms": round(calls["forward"], 5),
+            "backward_call_ms": round(calls["backward"], 5),
             "device": torch.cuda.get_device_name(device),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "msda_backward (C-ABI call: bucket sort, softmax stats if softmax, grad_value, grad_sample)",
-            "achieved": round(bwd_gbs, 1),
+            "kernel": "one msda_forward + msda_backward C-ABI call pair (forward kernel, bucket sort, "
+                      "grad_value, grad_sample), back to back on one stream",
+            "achieved": round(call_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
-            "frac": round(bwd_gbs / PEAK_HBM_GBS, 4),
-            "traffic": BACKWARD_TRAFFIC_BYTES if profiled else None,
-            "algorithmic_bytes_per_launch": bwd_bytes,
+            "frac": round(call_gbs / PEAK_HBM_GBS, 4),
+            "traffic": traffic,
+            "traffic_source": traffic_source,
+            "algorithmic_bytes_per_launch": fwd_bytes + bwd_bytes,
+            "launch_ms": round(calls["fwd_bwd"], 5),
+            "backward_call": {
+                "algorithmic_bytes": bwd_bytes,
+                "ms": round(calls["backward"], 5),
+                "achieved": round(bwd_gbs, 1),
+                "frac": round(bwd_gbs / PEAK_HBM_GBS, 4),
+            },
+            "gather": {
+                "kernel": "msda_forward_kernel: 4 corner rows of D channels per sample",
+                "bytes": corner_bytes,
+                "achieved": round(corner_gbs, 1),
+                "l1_peak": round(gather["l1"], 1),
+                "l2_peak": round(gather["l2"], 1),
+                "unit": "GB/s",
+                "frac_of_l2": round(corner_gbs / gather["l2"], 4),
+                "frac_of_l1": round(corner_gbs / gather["l1"], 4),
+                "peak_source": "random 64-byte row gathers from a 2 MiB (L2) and 16 KiB (L1) buffer, "
+                               "libmsda_probe.so, this run",
+            },
         },
     }
     if not args.no_cpu_baseline:

@@ -1,7 +1,9 @@
-"""Ahead-of-time build of the HIP library, libdeformops_amd.so, for gfx950.
+"""Ahead-of-time build of the HIP libraries for gfx950.
 
-The library is built in-tree (``deformops_amd/lib/``) with hipcc and loaded with
-ctypes; nothing is compiled at import or call time.
+libdeformops_amd.so is the MSDA library (the C ABI of include/deformops_amd.h);
+libmsda_probe.so holds the measurement probes bench.py rates the kernels against
+(include/msda_probe.h). Both are built in-tree (``deformops_amd/lib/``) with hipcc
+and loaded with ctypes; nothing is compiled at import or call time.
 
     python -m deformops_amd._build
 """
@@ -15,13 +17,15 @@ import sys
 import tempfile
 from pathlib import Path
 
-__all__ = ["ARCH", "HIPCC_FLAGS", "LIBRARY", "SOURCES", "build"]
+__all__ = ["ARCH", "HIPCC_FLAGS", "LIBRARY", "PROBE_LIBRARY", "SOURCES", "build"]
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_DIR = PACKAGE_DIR.parent
 SOURCES = [PACKAGE_DIR / "csrc" / "msda.hip"]
 INCLUDE_DIR = REPO_DIR / "include"
 LIBRARY = PACKAGE_DIR / "lib" / "libdeformops_amd.so"
+PROBE_SOURCES = [PACKAGE_DIR / "csrc" / "gather_probe.hip"]
+PROBE_LIBRARY = PACKAGE_DIR / "lib" / "libmsda_probe.so"
 ARCH = os.environ.get("DEFORMOPS_AMD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -48,17 +52,22 @@ def _hipcc() -> str:
 
 
 def build(*, verbose: bool = False) -> Path:
-    """Compile the library and atomically replace ``LIBRARY``; return its path.
+    """Compile both libraries, atomically replacing each; return the MSDA library's path.
 
     Raises
     ------
     subprocess.CalledProcessError
         If hipcc fails; the compiler output is in the exception.
     """
-    LIBRARY.parent.mkdir(parents=True, exist_ok=True)
-    fd, tmp = tempfile.mkstemp(prefix=LIBRARY.name + ".", suffix=".tmp", dir=LIBRARY.parent)
+    _compile(PROBE_SOURCES, PROBE_LIBRARY, verbose=verbose)
+    return _compile(SOURCES, LIBRARY, verbose=verbose)
+
+
+def _compile(sources: list[Path], target: Path, *, verbose: bool) -> Path:
+    target.parent.mkdir(parents=True, exist_ok=True)
+    fd, tmp = tempfile.mkstemp(prefix=target.name + ".", suffix=".tmp", dir=target.parent)
     os.close(fd)
-    cmd = [_hipcc(), *HIPCC_FLAGS, *map(str, SOURCES), "-o", tmp]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *map(str, sources), "-o", tmp]
     try:
         result = subprocess.run(cmd, capture_output=True, text=True, check=False)  # noqa: S603
         if verbose or result.returncode != 0:
@@ -68,11 +77,11 @@ def build(*, verbose: bool = False) -> Path:
                 print("\n".join(lines), file=sys.stderr)
         if result.returncode != 0:
             raise subprocess.CalledProcessError(result.returncode, cmd, result.stdout, result.stderr)
-        os.replace(tmp, LIBRARY)
+        os.replace(tmp, target)
     finally:
         if os.path.exists(tmp):
             os.unlink(tmp)
-    return LIBRARY
+    return target
 
 
 if __name__ == "__main__":

@@ -213,6 +213,42 @@ forward_op, backward_op = _define("msda", softmax=False)
 forward_softmax_op, backward_softmax_op = _define("msda_softmax", softmax=True)
 
 
+class _EagerMSDA(torch.autograd.Function):
+    """The private operators' forward and backward for plain eager calls.
+
+    The same two library calls as the registered operators, without the custom-op
+    dispatch around each (argument defaults, redispatch, the autograd wrapper), which
+    costs more host time than a small call's kernels. Traced, compiled, exported and
+    fake calls use the registered operators.
+    """
+
+    @staticmethod
+    def forward(ctx, value, spatial_shapes, level_start_index, loc, attn, softmax):  # noqa: ANN001, ANN205, PLR0913
+        ctx.save_for_backward(value, spatial_shapes, level_start_index, loc, attn)
+        ctx.softmax = softmax
+        return _forward_impl(value, spatial_shapes, level_start_index, loc, attn, int(loc.shape[4]),
+                             softmax=softmax)
+
+    @staticmethod
+    def backward(ctx, grad_output):  # noqa: ANN001, ANN205
+        value, spatial_shapes, level_start_index, loc, attn = ctx.saved_tensors
+        grad_value, grad_loc, grad_attn = _backward_impl(
+            value, spatial_shapes, level_start_index, loc, attn, grad_output, int(loc.shape[4]),
+            softmax=ctx.softmax,
+        )
+        return grad_value, None, None, grad_loc, grad_attn, None
+
+
+def _plain_eager(*tensors: Tensor) -> bool:
+    """Real tensors, no compile / trace, no dispatch or function mode, no functorch wrapper."""
+    if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack():  # noqa: SLF001
+        return False
+    if torch._C._is_torch_function_mode_enabled():  # noqa: SLF001
+        return False
+    wrapped = torch._C._functorch.is_functorch_wrapped_tensor  # noqa: SLF001
+    return all(type(t) in (Tensor, torch.nn.Parameter) and not wrapped(t) for t in tensors)
+
+
 # The adapter surface.
 
 
@@ -246,19 +282,14 @@ def forward(
         num_points = int(sampling_locations.shape[4])
     shapes, starts = _index_tables(spatial_shapes, level_start_index)
     loc = sampling_locations.to(_location_dtype(value.dtype, sampling_locations.dtype))
-    op = forward_softmax_op if softmax else forward_op
     with torch.autocast("cuda", enabled=False):
-        return op(
-            value.contiguous(),
-            shapes,
-            starts,
-            loc.contiguous(),
-            attention_weights.to(value.dtype).contiguous(),
-            chunk_step,
-            num_points,
-            channels_per_thread,
-            threads_per_block,
-        )
+        operands = (value.contiguous(), shapes, starts, loc.contiguous(),
+                    attention_weights.to(value.dtype).contiguous())
+        if _plain_eager(*operands):
+            _check_points(operands[3], num_points)
+            return _EagerMSDA.apply(*operands, softmax)
+        op = forward_softmax_op if softmax else forward_op
+        return op(*operands, chunk_step, num_points, channels_per_thread, threads_per_block)
 
 
 def _channels_per_lane(dtype: torch.dtype, head_dim: int) -> int:

@@ -1,20 +1,22 @@
 """Operand validation for the MSDA entry points.
 
-Restates the MSDA part of the reference's sources/deformops/core/sanitize.py:
-structural checks (rank, axis sizes, dtype, device; :276-392) run on every call
-and read metadata only; the level-table checks (:395-436) read the table back to
-the host, so they run only when ``DEFORMOPS_VALIDATE`` is set. Every failure is a
-``ValueError`` naming the operand, raised before any kernel launches.
+The contract is the reference's (sources/deformops/core/sanitize.py:56-146 for the
+layer sizes, :276-436 for a call): a malformed call raises ``ValueError`` naming
+the operand at fault, before any kernel launches, and reads tensor metadata only;
+the level-table contents are read back to the host only when ``DEFORMOPS_VALIDATE``
+is set, since that synchronizes the stream and breaks graph capture.
 
-The HIP kernels additionally treat a level whose table entry does not fit inside
-the value tensor as empty, so a malformed table yields zeros instead of an
-out-of-bounds access even when the value checks are off.
+The structural check here is one pass of shape unification. Each operand has a
+pattern over the symbols B (batch), S (positions), H (heads), D (channels), Q
+(queries), L (levels) and P (points); a symbol is bound by the first operand that
+has it and every later occurrence must agree. The HIP kernels treat a level whose
+table entry does not fit the value tensor as empty, so a malformed table yields
+zeros, never an out-of-bounds access, when the value checks are off.
 """
 
 from __future__ import annotations
 
 import os
-from collections.abc import Sequence
 from typing import TYPE_CHECKING
 
 if TYPE_CHECKING:
@@ -33,98 +35,83 @@ __all__ = [
 #: Enables the level-table checks; any value but a falsy spelling turns them on.
 VALIDATE_ENV_VAR = "DEFORMOPS_VALIDATE"
 
-_FALSY = frozenset({"0", "false", "no", "off", ""})
-
 
 def value_checks_enabled() -> bool:
-    """Whether to run the checks that read the level table back to the host.
+    """Whether the checks that read the level table back to the host run (off by default)."""
+    return os.getenv(VALIDATE_ENV_VAR, "0").strip().lower() not in {"", "0", "false", "no", "off"}
 
-    Off by default: the readback synchronizes the stream and breaks graph capture.
-    """
-    return os.getenv(VALIDATE_ENV_VAR, "0").strip().lower() not in _FALSY
+
+# Layer sizes.
 
 
 def check_positive(n: int, name: str) -> None:
-    """Raise ``ValueError`` unless ``n`` is a positive integer."""
-    if n <= 0:
-        msg = f"Expected {name} to be a positive integer, got: {n}"
-        raise ValueError(msg)
+    """``ValueError`` unless ``n`` is a positive integer."""
+    if not n > 0:
+        raise ValueError(f"{name} must be a positive integer; got {n}")
 
 
 def check_divisible(a: int, b: int) -> None:
-    """Raise ``ValueError`` unless ``b`` is non-zero and divides ``a``."""
-    if b == 0:
-        msg = "Expected a non-zero divisor, got: 0"
-        raise ValueError(msg)
-    if a % b != 0:
-        msg = f"Expected {a} to be divisible by {b}"
-        raise ValueError(msg)
+    """``ValueError`` unless ``b`` is non-zero and divides ``a``."""
+    if b == 0 or a % b:
+        raise ValueError(f"{a} is not divisible by {b}")
 
 
 def check_2power(n: int) -> None:
-    """Raise ``ValueError`` unless ``n`` is a positive power of two (reference
-    ``core/sanitize.py:56-74``)."""
-    if n <= 0:
-        msg = f"Expected a positive integer, got: {n}"
-        raise ValueError(msg)
-    if n & (n - 1):
-        msg = f"Expected a power of 2, got: {n}"
-        raise ValueError(msg)
+    """``ValueError`` unless ``n`` is a positive power of 2."""
+    if n <= 0 or n & (n - 1):
+        raise ValueError(f"expected a positive power of 2; got {n}")
 
 
 def check_msda_params(dim: int, num_heads: int, num_levels: int, num_points: int) -> None:
-    """Check the integers that size an MSDA layer (reference ``core/sanitize.py:120-146``)."""
-    check_positive(dim, "dim")
-    check_positive(num_heads, "num_heads")
-    check_positive(num_levels, "num_levels")
-    check_positive(num_points, "num_points")
+    """The integers that size an MSDA layer: all positive, ``dim`` split evenly over heads."""
+    for name, n in (("dim", dim), ("num_heads", num_heads), ("num_levels", num_levels),
+                    ("num_points", num_points)):
+        check_positive(n, name)
     check_divisible(dim, num_heads)
 
 
-def _rank(name: str, tensor: Tensor, allowed: tuple[int, ...]) -> None:
-    if tensor.dim() not in allowed:
-        wanted = " or ".join(str(a) for a in allowed)
-        msg = (
-            f"{name} must be {wanted}-dimensional, got {tensor.dim()} dimensions "
-            f"with shape {tuple(tensor.shape)}"
-        )
-        raise ValueError(msg)
+# One call.
+
+#: Axis patterns of the five operands: symbols bind on first sight, integers are
+#: fixed sizes. attention_weights takes either pattern.
+_PATTERNS: tuple[tuple[str, tuple[tuple[str | int, ...], ...]], ...] = (
+    ("value", (("B", "S", "H", "D"),)),
+    ("spatial_shapes", (("L", 2),)),
+    ("level_start_index", (("L",),)),
+    ("sampling_locations", (("B", "Q", "H", "L", "P", 2),)),
+    ("attention_weights", (("B", "Q", "H", "LP"), ("B", "Q", "H", "L", "P"))),
+)
+
+_MEANING = {
+    "B": "the batch of value",
+    "H": "the heads of value",
+    "L": "the levels (rows of spatial_shapes)",
+    "Q": "the queries of sampling_locations",
+    "P": "the points of sampling_locations",
+    "LP": "levels x points of sampling_locations",
+}
 
 
-def _axis(name: str, tensor: Tensor, axis: int, expected: int, why: str) -> None:
-    actual = tensor.size(axis)
-    if actual != expected:
-        msg = (
-            f"{name} has size {actual} on axis {axis}, expected {expected} ({why}). "
-            f"Full shape: {tuple(tensor.shape)}"
-        )
-        raise ValueError(msg)
-
-
-def _floating(name: str, tensor: Tensor) -> None:
-    if not tensor.is_floating_point():
-        msg = f"{name} must be a floating-point tensor, got dtype {tensor.dtype}"
-        raise ValueError(msg)
-
-
-def _integral(name: str, tensor: Tensor) -> None:
-    if tensor.is_floating_point() or tensor.is_complex():
-        msg = (
-            f"{name} must be an integer tensor (it indexes the value tensor), "
-            f"got dtype {tensor.dtype}"
-        )
-        raise ValueError(msg)
-
-
-def _same_device(named: Sequence[tuple[str, Tensor]]) -> None:
-    first_name, first = named[0]
-    for name, tensor in named[1:]:
-        if tensor.device != first.device:
-            msg = (
-                f"{name} is on {tensor.device} but {first_name} is on {first.device}; "
-                f"all operands must share one device"
+def _unify(name: str, shape: tuple[int, ...], patterns: tuple[tuple[str | int, ...], ...],
+           bound: dict[str, int]) -> None:
+    """Match ``shape`` to the pattern of its rank; bind new symbols, check old ones."""
+    pattern = next((p for p in patterns if len(p) == len(shape)), None)
+    if pattern is None:
+        ranks = " or ".join(str(len(p)) for p in patterns)
+        raise ValueError(f"{name} must have {ranks} dimensions; got shape {tuple(shape)}")
+    for axis, (symbol, size) in enumerate(zip(pattern, shape)):
+        if isinstance(symbol, int):
+            want, why = symbol, "its fixed size"
+        elif symbol in bound:
+            want, why = bound[symbol], _MEANING.get(symbol, symbol)
+        else:
+            bound[symbol] = size
+            continue
+        if size != want:
+            raise ValueError(
+                f"{name} has {size} entries on axis {axis} where {want} are expected "
+                f"({why}); its shape is {tuple(shape)}"
             )
-            raise ValueError(msg)
 
 
 def check_msda_call(
@@ -134,112 +121,67 @@ def check_msda_call(
     sampling_locations: Tensor,
     attention_weights: Tensor,
 ) -> None:
-    """Validate the five MSDA operands; raise ``ValueError`` on the first mismatch.
+    """Validate the five MSDA operands; ``ValueError`` names the first operand at fault.
 
-    Shapes: value ``(B, S, H, D)``, spatial_shapes ``(L, 2)`` integer,
-    level_start_index ``(L,)`` integer, sampling_locations ``(B, Q, H, L, P, 2)``
-    floating, attention_weights ``(B, Q, H, L * P)`` or ``(B, Q, H, L, P)`` in the
-    dtype of value. All on one device.
+    value ``(B, S, H, D)`` floating; spatial_shapes ``(L, 2)`` and level_start_index
+    ``(L,)`` integer; sampling_locations ``(B, Q, H, L, P, 2)`` floating;
+    attention_weights ``(B, Q, H, L * P)`` or ``(B, Q, H, L, P)`` in value's dtype;
+    one device for all.
     """
-    _rank("value", value, (4,))
-    _rank("spatial_shapes", spatial_shapes, (2,))
-    _rank("level_start_index", level_start_index, (1,))
-    _rank("sampling_locations", sampling_locations, (6,))
-    _rank("attention_weights", attention_weights, (4, 5))
+    operands = (value, spatial_shapes, level_start_index, sampling_locations, attention_weights)
+    bound: dict[str, int] = {}
+    for (name, patterns), tensor in zip(_PATTERNS, operands):
+        if name == "attention_weights" and "L" in bound and "P" in bound:
+            bound["LP"] = bound["L"] * bound["P"]
+        _unify(name, tuple(tensor.shape), patterns, bound)
 
-    _axis("spatial_shapes", spatial_shapes, 1, 2, "each row is (height, width)")
-    _axis(
-        "sampling_locations",
-        sampling_locations,
-        5,
-        2,
-        "each location is a normalized (x, y) pair",
-    )
-
-    batch, _, heads, _ = value.shape
-    levels = spatial_shapes.size(0)
-    _, queries, _, loc_levels, points, _ = sampling_locations.shape
-
-    _axis("level_start_index", level_start_index, 0, levels, "one entry per level")
-    _axis("sampling_locations", sampling_locations, 0, batch, "batch of value")
-    _axis("sampling_locations", sampling_locations, 2, heads, "heads of value")
-    _axis("sampling_locations", sampling_locations, 3, levels, "rows of spatial_shapes")
-    _axis("attention_weights", attention_weights, 0, batch, "batch of value")
-    _axis("attention_weights", attention_weights, 1, queries, "queries of locations")
-    _axis("attention_weights", attention_weights, 2, heads, "heads of value")
-    if attention_weights.dim() == 4:
-        _axis(
-            "attention_weights",
-            attention_weights,
-            3,
-            loc_levels * points,
-            "levels x points of sampling_locations",
-        )
-    else:
-        _axis("attention_weights", attention_weights, 3, loc_levels, "levels of sampling_locations")
-        _axis("attention_weights", attention_weights, 4, points, "points of sampling_locations")
-
-    _integral("spatial_shapes", spatial_shapes)
-    _integral("level_start_index", level_start_index)
-    _floating("value", value)
-    _floating("attention_weights", attention_weights)
+    for (name, _), tensor in zip(_PATTERNS, operands):
+        integral = name in ("spatial_shapes", "level_start_index")
+        if integral and (tensor.is_floating_point() or tensor.is_complex()):
+            raise ValueError(f"{name} indexes the value tensor and must be integer; got {tensor.dtype}")
+        if not integral and not tensor.is_floating_point():
+            raise ValueError(f"{name} must be floating point; got {tensor.dtype}")
     if attention_weights.dtype != value.dtype:
-        msg = (
-            f"attention_weights has dtype {attention_weights.dtype} but value has "
-            f"{value.dtype}; mixed input dtypes are not supported. Cast the operands "
-            f"to a common dtype, or wrap the call in autocast"
+        raise ValueError(
+            f"attention_weights is {attention_weights.dtype} while value is {value.dtype}; "
+            f"give both one dtype (or run the call under autocast)"
         )
-        raise ValueError(msg)
-    _floating("sampling_locations", sampling_locations)
-    _same_device(
-        [
-            ("value", value),
-            ("spatial_shapes", spatial_shapes),
-            ("level_start_index", level_start_index),
-            ("sampling_locations", sampling_locations),
-            ("attention_weights", attention_weights),
-        ]
-    )
+    devices = {tensor.device for tensor in operands}
+    if len(devices) > 1:
+        where = ", ".join(f"{name} on {t.device}" for (name, _), t in zip(_PATTERNS, operands))
+        raise ValueError(f"the operands must share one device; got {where}")
 
-    if value_checks_enabled() and _has_values(spatial_shapes, level_start_index):
-        _check_level_layout(value, spatial_shapes, level_start_index)
+    if value_checks_enabled() and _readable(spatial_shapes, level_start_index):
+        _check_level_table(value, spatial_shapes, level_start_index)
 
 
-def _has_values(*tensors: Tensor) -> bool:
-    """Whether the tensors hold readable data: not fake and not being traced."""
+def _readable(*tensors: Tensor) -> bool:
+    """Whether the tensors hold data the host can read: not traced, fake or meta."""
     import torch  # noqa: PLC0415
     from torch._subclasses.fake_tensor import is_fake  # noqa: PLC0415
 
     if torch.compiler.is_compiling():
         return False
-    return not any(is_fake(t) or t.device.type == "meta" for t in tensors)
+    return all(t.device.type != "meta" and not is_fake(t) for t in tensors)
 
 
-def _check_level_layout(value: Tensor, spatial_shapes: Tensor, level_start_index: Tensor) -> None:
-    """The levels must be non-empty, start at the running offset and tile value."""
-    shapes = spatial_shapes.detach().cpu().tolist()
-    starts = level_start_index.detach().cpu().tolist()
-    for level, (height, width) in enumerate(shapes):
-        if height <= 0 or width <= 0:
-            msg = (
-                f"spatial_shapes row {level} is ({height}, {width}); every level "
-                f"must have a positive height and width"
-            )
-            raise ValueError(msg)
-    expected, running = [], 0
-    for height, width in shapes:
-        expected.append(running)
-        running += height * width
-    if starts != expected:
-        msg = (
-            f"level_start_index {starts} is not the exclusive prefix sum of the level "
-            f"sizes {[h * w for h, w in shapes]}; expected {expected}"
+def _check_level_table(value: Tensor, spatial_shapes: Tensor, level_start_index: Tensor) -> None:
+    """The levels are non-empty, laid end to end from 0, and exactly fill value's S axis."""
+    sizes = [(int(h), int(w)) for h, w in spatial_shapes.detach().cpu().tolist()]
+    starts = [int(s) for s in level_start_index.detach().cpu().tolist()]
+    empty = [i for i, (h, w) in enumerate(sizes) if h <= 0 or w <= 0]
+    if empty:
+        raise ValueError(f"spatial_shapes has an empty level at row {empty[0]}: {sizes[empty[0]]}")
+    offsets = [0]
+    for h, w in sizes:
+        offsets.append(offsets[-1] + h * w)
+    if starts != offsets[:-1]:
+        raise ValueError(
+            f"level_start_index is {starts}, but levels of sizes {[h * w for h, w in sizes]} laid end "
+            f"to end start at {offsets[:-1]}"
         )
-        raise ValueError(msg)
-    if running != value.size(1):
-        msg = (
-            f"spatial_shapes describes {running} positions but value has "
-            f"{value.size(1)} on its spatial axis; the levels must tile the value "
-            f"tensor exactly"
+    if offsets[-1] != value.shape[1]:
+        raise ValueError(
+            f"spatial_shapes covers {offsets[-1]} positions but value has {value.shape[1]} on its "
+            f"spatial axis"
         )
-        raise ValueError(msg)

@@ -1,16 +1,19 @@
-"""Backend registry: one per operator, mapping :class:`Backend` members to callables.
+"""The backend table of one operator.
 
-Behaviour follows the reference's ``Registry`` (sources/deformops/registry/_dispatch.py:
-122-454): an explicit ``backend=`` runs that backend or raises
-:class:`NoBackendError`; ``backend=None`` runs the first candidate of the
-operator's selection policy that is registered, supports the call and can load
-its kernel, memoized per call context; raw strings are rejected with
-``TypeError``.
+Interface of the reference's registry (sources/deformops/registry/_dispatch.py:
+35-454): the ``Backend`` enum, ``Resolution`` and ``LoadedBackend`` records, and a
+``Registry`` whose ``register``, ``load``, ``resolve``, ``run_selected`` and
+``__call__`` behave as there. An explicit ``backend=`` runs that backend or raises
+``NoBackendError``; ``backend=None`` runs the first candidate of the operator's
+policy that is registered, supports the call and loads its kernels; a raw string
+for ``backend`` is a ``TypeError``.
 
-This build registers a single backend, ``Backend.HIP`` (``Backend.CUDA`` is an
-alias of it, so code written for the reference's CUDA backend runs the HIP
-kernels). ``TRITON`` and ``EAGER`` exist so such code still imports; asking for
-them raises ``NoBackendError`` with the reason.
+This build ships one backend, the HIP kernels, so the table is small and the
+choice needs no memo: a policy names one or two candidates, and checking them is a
+dictionary lookup, a predicate on the call's context and an already-loaded
+library. ``Backend.CUDA`` is an alias of ``Backend.HIP``, so code written for the
+reference's CUDA backend runs the HIP kernels; ``TRITON`` and ``EAGER`` exist so
+that such code imports, and asking for them says why they are absent.
 """
 
 from __future__ import annotations
@@ -18,11 +21,10 @@ from __future__ import annotations
 import dataclasses
 import importlib
 import inspect
-import logging
 import os
 import threading
 import warnings
-from collections.abc import Callable, Mapping, Sequence
+from collections.abc import Callable, Iterable, Mapping
 from enum import Enum
 from typing import Any
 
@@ -30,17 +32,14 @@ from ..core.errors import BackendFallbackWarning, KernelNotProvidedError, NoBack
 
 __all__ = ["Backend", "LoadedBackend", "Registry", "Resolution"]
 
-logger = logging.getLogger(__name__)
-
 #: Set to a falsy value to silence :class:`BackendFallbackWarning`.
 FALLBACK_WARNINGS_ENV_VAR = "DEFORMOPS_FALLBACK_WARNINGS"
 
-_FALSY = frozenset({"0", "false", "no", "off"})
-
 
 class Backend(str, Enum):
-    """Compute backends. ``CUDA`` is an alias of ``HIP`` (torch's ROCm device type is
-    ``"cuda"``); ``TRITON`` and ``EAGER`` are never registered in this build."""
+    """Compute backends. ``CUDA`` is an alias of ``HIP`` (torch's device type on ROCm is
+    ``"cuda"``, and ``Backend("cuda")`` is ``HIP``); ``TRITON`` and ``EAGER`` are never
+    registered in this build."""
 
     HIP = "hip"
     CUDA = "hip"
@@ -49,29 +48,16 @@ class Backend(str, Enum):
 
     @classmethod
     def _missing_(cls, value: object) -> Backend | None:
-        if value == "cuda":
-            return cls.HIP
-        return None
+        return cls.HIP if value == "cuda" else None
 
     def __str__(self) -> str:
         return self.value
 
 
-#: Where the adapter of each registered backend lives.
-_ADAPTER_MODULES: dict[Backend, str] = {Backend.HIP: "deformops_amd.backends.hip"}
-
-#: Why the other backends are absent.
-_ABSENT_REASON = (
-    "it is not part of this build, which runs MSDA only on AMD GPUs through its "
-    "HIP kernels (Backend.HIP)"
-)
-
-Candidate = Backend | tuple[Backend, Mapping[str, Any]]
-
-
 @dataclasses.dataclass(frozen=True)
 class Resolution:
-    """The backend a call runs on, its options, and the candidates passed over."""
+    """The backend a call runs on, the options the policy gives it, and the
+    ``(backend, reason)`` of every candidate it preferred that could not run."""
 
     backend: Backend
     options: dict[str, Any]
@@ -80,57 +66,89 @@ class Resolution:
 
 @dataclasses.dataclass(frozen=True)
 class LoadedBackend:
-    """What :meth:`Registry.load` made ready: operator, backend and library path."""
+    """What :meth:`Registry.load` made ready: the operator, the backend and the path of
+    its kernel library (``None`` for a backend without one)."""
 
     operator: str
     backend: Backend
     library: str | None
 
 
-def _normalize(selected: Candidate | Sequence[Candidate]) -> list[tuple[Backend, dict[str, Any]]]:
-    items: Sequence[Candidate]
-    if isinstance(selected, Backend):
-        items = [selected]
-    elif isinstance(selected, tuple) and len(selected) == 2 and isinstance(selected[0], Backend):  # noqa: PLR2004
-        items = [selected]  # type: ignore[list-item]
-    else:
-        items = selected  # type: ignore[assignment]
-    out: list[tuple[Backend, dict[str, Any]]] = []
-    for item in items:
+@dataclasses.dataclass
+class _Entry:
+    run: Callable[..., Any]
+    supports: Callable[[Any], bool] | None = None
+    load: Callable[..., Any] | None = None
+
+
+#: Packages that hold each backend's adapter module (``<package>.<operator>``).
+_ADAPTERS: dict[Backend, str] = {Backend.HIP: "deformops_amd.backends.hip"}
+
+_NOT_BUILT = (
+    "it is not part of this build, which runs MSDA only on AMD GPUs through its HIP "
+    "kernels (Backend.HIP)"
+)
+
+
+def _candidates(picked: Any) -> Iterable[tuple[Backend, dict[str, Any]]]:
+    """A policy's answer as ``(backend, options)`` pairs: it may name one backend, one
+    ``(backend, options)`` pair, or a sequence of either."""
+    if isinstance(picked, Backend) or (isinstance(picked, tuple) and picked and isinstance(picked[0], Backend)
+                                       and len(picked) == 2 and isinstance(picked[1], Mapping)):
+        picked = [picked]
+    for item in picked:
         if isinstance(item, Backend):
-            out.append((item, {}))
+            yield item, {}
         else:
-            out.append((item[0], dict(item[1])))
-    return out
+            yield item[0], dict(item[1])
+
+
+def _require_backend(backend: object, *, allow_none: bool) -> None:
+    if backend is None and allow_none:
+        return
+    if not isinstance(backend, Backend):
+        raise TypeError(
+            f"backend must be a Backend member{' or None' if allow_none else ''}, not "
+            f"{type(backend).__name__} (raw strings are not accepted)"
+        )
 
 
 class Registry:
-    """Backends of one operator, with a selection policy for ``backend=None``."""
+    """The backends of one operator and the policy that picks one for ``backend=None``.
+
+    Parameters
+    ----------
+    name
+        The operator's name, also the adapter module name under each backend package.
+    context_of
+        Builds the selection context from a call's arguments, validating them.
+    select
+        The policy: context to candidate backends, best first.
+    describe
+        A function whose docstring and signature document the operator.
+    """
 
     def __init__(
         self,
         name: str,
         *,
         context_of: Callable[..., Any],
-        select: Callable[[Any], Candidate | Sequence[Candidate]],
+        select: Callable[[Any], Any],
         describe: Callable[..., Any] | None = None,
     ) -> None:
         self.name = name
+        self._context_of = context_of
+        self._select = select
+        self._entries: dict[Backend, _Entry] = {}
+        self._absent: dict[Backend, str] = {}
+        self._route: Callable[..., Any] | None = None
+        self._adapters_ready = False
+        self._lock = threading.Lock()
         if describe is not None:
             self.__doc__ = describe.__doc__
             self.__signature__ = inspect.signature(describe)
-        self._handlers: dict[Backend, Callable[..., Any]] = {}
-        self._supports: dict[Backend, Callable[[Any], bool]] = {}
-        self._loaders: dict[Backend, Callable[..., Any]] = {}
-        self._absent: dict[Backend, str] = {}
-        self._context_of = context_of
-        self._select = select
-        self._memo: dict[Any, Resolution] = {}
-        self._imported = False
-        self._lock = threading.RLock()
-        self._route: Callable[..., Any] | None = None
 
-    # Registration.
+    # The table.
 
     def register(
         self,
@@ -140,190 +158,142 @@ class Registry:
         supports: Callable[[Any], bool] | None = None,
         load: Callable[..., Any] | None = None,
     ) -> None:
-        """File ``op_handle`` under ``backend``; ``supports`` and ``load`` are optional."""
-        if not isinstance(backend, Backend):
-            msg = (
-                f"backend must be a Backend member, got {type(backend).__name__!r}. "
-                f"Raw strings are not permitted."
-            )
-            raise TypeError(msg)
-        self._handlers[backend] = op_handle
+        """File ``op_handle`` as ``backend``'s implementation, with an optional
+        ``supports(context)`` predicate and ``load(download=, compile=)`` hook."""
+        _require_backend(backend, allow_none=False)
+        self._entries[backend] = _Entry(op_handle, supports, load)
         self._absent.pop(backend, None)
-        if supports is not None:
-            self._supports[backend] = supports
-        if load is not None:
-            self._loaders[backend] = load
-        self._memo.clear()
 
     def mark_unavailable(self, backend: Backend, reason: str) -> None:
-        """Record why ``backend`` is not registered, for error messages."""
-        if backend not in self._handlers:
+        """Record why ``backend`` is not registered; error messages quote it."""
+        if backend not in self._entries:
             self._absent[backend] = reason
 
     def route_selected_calls(self, route: Callable[..., Any]) -> None:
-        """Send every ``backend=None`` call through ``route`` (a public operator)."""
+        """Send ``backend=None`` calls through ``route`` (the public operator)."""
         self._route = route
 
     def _import_adapters(self) -> None:
-        if self._imported:
+        if self._adapters_ready:
             return
         with self._lock:
-            if self._imported:
+            if self._adapters_ready:
                 return
-            for backend in Backend:
-                module = _ADAPTER_MODULES.get(backend)
-                if module is None:
-                    self.mark_unavailable(backend, _ABSENT_REASON)
+            for backend in (Backend.HIP, Backend.TRITON, Backend.EAGER):
+                package = _ADAPTERS.get(backend)
+                if package is None:
+                    self.mark_unavailable(backend, _NOT_BUILT)
                     continue
                 try:
-                    importlib.import_module(f"{module}.{self.name}")
-                except Exception as error:  # noqa: BLE001
-                    logger.debug("Failed to import %s.%s", module, self.name, exc_info=True)
+                    importlib.import_module(f"{package}.{self.name}")
+                except Exception as error:  # noqa: BLE001 - reported, and the backend marked absent
                     reason = f"its adapter failed to import ({type(error).__name__}: {error})"
                     self.mark_unavailable(backend, reason)
-                    warnings.warn(
-                        f"The {backend.value!r} backend for {self.name!r} is unavailable: {reason}",
-                        RuntimeWarning,
-                        stacklevel=3,
-                    )
-            self._imported = True
+                    warnings.warn(f"{self.name}: the {backend.value!r} backend is unavailable: {reason}",
+                                  RuntimeWarning, stacklevel=3)
+            self._adapters_ready = True
 
     # Queries.
 
     def is_registered(self, backend: Backend) -> bool:
         self._import_adapters()
-        return backend in self._handlers
+        return backend in self._entries
 
     def get(self, backend: Backend) -> Callable[..., Any] | None:
         self._import_adapters()
-        return self._handlers.get(backend)
+        entry = self._entries.get(backend)
+        return None if entry is None else entry.run
 
     def available(self) -> list[str]:
         self._import_adapters()
-        return sorted({b.value for b in self._handlers})
+        return sorted({backend.value for backend in self._entries})
 
     def unavailable_reason(self, backend: Backend) -> str:
         return self._absent.get(backend, "it is not registered on this host")
 
-    def load(
-        self,
-        backend: Backend,
-        *,
-        download: bool | None = None,
-        compile: bool | str | None = None,  # noqa: A002
-    ) -> LoadedBackend:
-        """Make ``backend`` ready before the first call and report its library."""
-        if not isinstance(backend, Backend):
-            msg = f"backend must be a Backend member, got {type(backend).__name__!r}"
-            raise TypeError(msg)
-        if not self.is_registered(backend):
-            msg = (
-                f"The {backend.value!r} backend for {self.name} is unavailable: "
-                f"{self.unavailable_reason(backend)}."
-            )
-            raise NoBackendError(msg)
-        loader = self._loaders.get(backend)
-        library = None
-        if loader is not None:
-            library = str(loader(download=download, compile=compile))
+    def load(self, backend: Backend, *, download: bool | None = None,
+             compile: bool | str | None = None) -> LoadedBackend:  # noqa: A002
+        """Make ``backend`` ready before its first call; report its library."""
+        _require_backend(backend, allow_none=False)
+        self._import_adapters()
+        entry = self._entries.get(backend)
+        if entry is None:
+            raise NoBackendError(f"{self.name}: the {backend.value!r} backend is unavailable: "
+                                 f"{self.unavailable_reason(backend)}.")
+        library = None if entry.load is None else str(entry.load(download=download, compile=compile))
         return LoadedBackend(self.name, backend, library)
 
-    # Selection.
+    # Choosing.
 
-    def _supports_call(self, backend: Backend, context: Any) -> bool:
-        predicate = self._supports.get(backend)
-        return predicate is None or bool(predicate(context))
+    def _refusal(self, backend: Backend, context: Any) -> str | None:
+        """Why ``backend`` cannot run a call with ``context``, or ``None`` when it can
+        (its kernels then are loaded)."""
+        entry = self._entries.get(backend)
+        if entry is None:
+            return self.unavailable_reason(backend)
+        if entry.supports is not None and not entry.supports(context):
+            return "it does not support this call"
+        if entry.load is not None:
+            try:
+                entry.load()
+            except KernelNotProvidedError as error:
+                return str(error)
+        return None
 
-    def _negotiate(self, context: Any) -> Resolution:
+    def _choose(self, context: Any) -> Resolution:
         rejected: list[tuple[Backend, str]] = []
-        for backend, options in _normalize(self._select(context)):
-            if backend not in self._handlers:
-                rejected.append((backend, self.unavailable_reason(backend)))
+        for backend, options in _candidates(self._select(context)):
+            reason = self._refusal(backend, context)
+            if reason is not None:
+                rejected.append((backend, reason))
                 continue
-            if not self._supports_call(backend, context):
-                rejected.append((backend, "it does not support this call"))
-                continue
-            loader = self._loaders.get(backend)
-            if loader is not None:
-                try:
-                    loader()
-                except KernelNotProvidedError as error:
-                    rejected.append((backend, str(error)))
-                    continue
-            if rejected and os.getenv(FALLBACK_WARNINGS_ENV_VAR, "").strip().lower() not in _FALSY:
-                warnings.warn(
-                    f"{self.name}: running the {backend.value!r} backend because "
-                    + "; ".join(f"{b.value!r} was passed over: {r}" for b, r in rejected)
-                    + f". Set {FALLBACK_WARNINGS_ENV_VAR}=0 to silence this warning.",
-                    BackendFallbackWarning,
-                    stacklevel=4,
-                )
+            if rejected and os.getenv(FALLBACK_WARNINGS_ENV_VAR, "1").strip().lower() not in {"0", "false", "no", "off"}:
+                passed = "; ".join(f"{b.value!r}: {why}" for b, why in rejected)
+                warnings.warn(f"{self.name} runs on {backend.value!r}, passing over {passed}. Set "
+                              f"{FALLBACK_WARNINGS_ENV_VAR}=0 to silence this.", BackendFallbackWarning,
+                              stacklevel=4)
             return Resolution(backend, options, tuple(rejected))
-        details = "; ".join(f"{b.value!r}: {r}" for b, r in rejected)
-        msg = (
-            f"No backend can run this {self.name} call ({context!r}). "
-            f"Candidates in order of preference: {details or 'none'}."
-        )
-        raise NoBackendError(msg)
+        tried = "; ".join(f"{b.value!r}: {why}" for b, why in rejected) or "none"
+        raise NoBackendError(f"No backend can run this {self.name} call ({context!r}). Candidates: {tried}.")
 
-    def _resolved(self, context: Any) -> Resolution:
-        hit = self._memo.get(context)
-        if hit is None:
-            hit = self._negotiate(context)
-            self._memo[context] = hit
-        return hit
-
-    @staticmethod
-    def _check_backend_argument(backend: object) -> None:
-        if backend is not None and not isinstance(backend, Backend):
-            msg = (
-                f"backend argument must be a Backend member or None, got "
-                f"{type(backend).__name__!r}. Raw strings are not permitted."
+    def _explicit(self, backend: Backend, context: Any) -> _Entry:
+        entry = self._entries.get(backend)
+        if entry is None:
+            raise NoBackendError(
+                f"{self.name}: the {backend.value!r} backend is unavailable: {self.unavailable_reason(backend)}. "
+                f"Registered: {self.available()}."
             )
-            raise TypeError(msg)
-
-    def _explicit(self, backend: Backend, context: Any) -> Callable[..., Any]:
-        handler = self._handlers.get(backend)
-        if handler is None:
-            msg = (
-                f"The {backend.value!r} backend for {self.name} is unavailable: "
-                f"{self.unavailable_reason(backend)}. Registered backends: {self.available()}."
-            )
-            raise NoBackendError(msg)
-        if not self._supports_call(backend, context):
-            msg = f"The {backend.value!r} backend does not support this {self.name} call: {context!r}"
-            raise NoBackendError(msg)
-        return handler
+        if entry.supports is not None and not entry.supports(context):
+            raise NoBackendError(f"{self.name}: the {backend.value!r} backend does not support this call: "
+                                 f"{context!r}")
+        return entry
 
     def resolve(self, *args: Any, backend: Backend | None = None, **kwargs: Any) -> Resolution:
-        """Report which backend a call with these arguments would run on."""
-        self._check_backend_argument(backend)
+        """The backend a call with these arguments would run on, without running it."""
+        _require_backend(backend, allow_none=True)
         self._import_adapters()
         context = self._context_of(*args, **kwargs)
-        if backend is not None:
-            self._explicit(backend, context)
-            loader = self._loaders.get(backend)
-            if loader is not None:
-                loader()
-            return Resolution(backend, {})
-        return self._resolved(context)
+        if backend is None:
+            return self._choose(context)
+        entry = self._explicit(backend, context)
+        if entry.load is not None:
+            entry.load()
+        return Resolution(backend, {})
 
     def run_selected(self, *args: Any, **kwargs: Any) -> Any:
-        """Run a call on the policy's backend, bypassing any route."""
+        """Run a call on the policy's choice, never through the route."""
         self._import_adapters()
-        context = self._context_of(*args, **kwargs)
-        resolution = self._resolved(context)
-        return self._handlers[resolution.backend](*args, **{**resolution.options, **kwargs})
+        choice = self._choose(self._context_of(*args, **kwargs))
+        return self._entries[choice.backend].run(*args, **{**choice.options, **kwargs})
 
     def __call__(self, *args: Any, backend: Backend | None = None, **kwargs: Any) -> Any:
-        """Run the operator on the requested backend, or the selected one."""
-        self._check_backend_argument(backend)
-        if backend is not None:
-            self._import_adapters()
-            context = self._context_of(*args, **kwargs)
-            return self._explicit(backend, context)(*args, **kwargs)
-        if self._route is not None:
-            return self._route(*args, **kwargs)
-        return self.run_selected(*args, **kwargs)
+        """Run the operator on ``backend``, or on the policy's choice for ``None``."""
+        _require_backend(backend, allow_none=True)
+        if backend is None:
+            if self._route is not None:
+                return self._route(*args, **kwargs)
+            return self.run_selected(*args, **kwargs)
+        self._import_adapters()
+        return self._explicit(backend, self._context_of(*args, **kwargs)).run(*args, **kwargs)
 
     apply = __call__

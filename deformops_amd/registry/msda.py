@@ -1,12 +1,17 @@
-r"""Multi-scale deformable attention (MSDA): call context, policy and registry.
+r"""Multi-scale deformable attention (MSDA): call context, selection policy, entry points.
 
-``msda`` is the entry point every caller uses; it keeps the reference's call
-surface (sources/deformops/registry/msda.py:274-361): five positional tensors,
-the keywords ``method``, ``softmax``, ``chunk_step`` and ``backend``, and the
-backend options ``num_points``, ``channels_per_thread``, ``threads_per_block`` and
-``fp32acc``, which this build accepts and ignores. ``torch.ops.deformops.msda`` and
-``torch.ops.deformops.msda_softmax`` are the public operators with the reference's
-schema (:365-412).
+``msda`` is the entry every caller uses. Its call surface is the reference's
+(sources/deformops/registry/msda.py:274-361): five positional tensors, the keywords
+``method``, ``softmax``, ``chunk_step`` and ``backend``, and the backend options
+``num_points``, ``channels_per_thread``, ``threads_per_block`` and ``fp32acc``,
+which the HIP kernels accept and ignore. ``torch.ops.deformops.msda`` and
+``msda_softmax`` are the public operators.
+
+A ``backend=None`` call goes through the public operator, so that ``torch.compile``,
+``torch.export``, vmap and fake tensors see it. A plain eager call (real tensors, no
+tracing, no dispatch or function mode) would only re-enter this module through the
+operator's composite kernel and validate its operands twice; it runs the selected
+backend directly instead.
 """
 
 from __future__ import annotations
@@ -20,7 +25,7 @@ from torch import Tensor
 from ..core.runtime import Method, is_training_from, resolve_method, sm_version_for
 from ..core.sanitize import check_msda_call
 from ._dispatch import Backend, Registry
-from ._public_ops import define_public_op
+from ._public import define_public_op
 
 __all__ = [
     "MSDABackend",
@@ -39,11 +44,9 @@ MSDAMethod = Method
 
 @dataclasses.dataclass(frozen=True)
 class MSDAContext:
-    """Summary of one call, the memo key of backend selection.
-
-    ``num_queries`` is left out of equality so that varying resolutions do not
-    grow the memo (reference registry/msda.py:40-88).
-    """
+    """What backend selection knows of a call (fields as the reference's,
+    registry/msda.py:40-88). ``num_queries`` is left out of equality, and is 0 when
+    symbolic; ``head_dim`` is 0 when unknown."""
 
     device: torch.device
     num_levels: int
@@ -54,28 +57,22 @@ class MSDAContext:
     is_training: bool
     num_queries: int = dataclasses.field(compare=False)
     method: Method = Method.LINEAR
-    #: Channels per head; 0 when unknown.
     head_dim: int = 0
 
     @classmethod
-    def from_call(
-        cls,
-        value: Tensor,
-        spatial_shapes: Tensor,
-        sampling_locations: Tensor,
-        attention_weights: Tensor,
-        method: Method,
-    ) -> MSDAContext:
-        queries: int | torch.SymInt = sampling_locations.shape[1]
+    def from_call(cls, value: Tensor, spatial_shapes: Tensor, sampling_locations: Tensor,
+                  attention_weights: Tensor, method: Method) -> MSDAContext:
+        """The context of a call; the tensors may be fake, with symbolic sizes."""
+        B, Q, H, L, P, _ = sampling_locations.shape
         return cls(
             device=value.device,
             num_levels=int(spatial_shapes.shape[0]),
-            num_heads=int(value.shape[2]),
-            num_points=int(sampling_locations.shape[4]),
+            num_heads=int(H),
+            num_points=int(P),
             dtype=value.dtype,
             sm_version=sm_version_for(value.device),
             is_training=is_training_from(value, sampling_locations, attention_weights),
-            num_queries=0 if isinstance(queries, torch.SymInt) else int(queries),
+            num_queries=Q if isinstance(Q, int) else 0,
             method=method,
             head_dim=int(value.shape[3]),
         )
@@ -83,115 +80,79 @@ class MSDAContext:
 
 @runtime_checkable
 class MSDABackend(Protocol):
-    """What a backend adapter provides (reference registry/msda.py:91-146)."""
+    """An adapter a layer can call directly (reference registry/msda.py:91-146)."""
 
     @property
     def name(self) -> str: ...
 
     def supports(self, context: MSDAContext) -> bool: ...
 
-    def forward(
-        self,
-        value: Tensor,
-        spatial_shapes: Tensor,
-        level_start_index: Tensor,
-        sampling_locations: Tensor,
-        attention_weights: Tensor,
-        chunk_step: int,
-        method: Method,
-    ) -> Tensor: ...
+    def forward(self, value: Tensor, spatial_shapes: Tensor, level_start_index: Tensor,
+                sampling_locations: Tensor, attention_weights: Tensor, chunk_step: int,
+                method: Method) -> Tensor: ...
 
 
 def msda_method_to_aggregate(method: str | Method) -> int:
-    """The integer code of a method: 1 for softmax, 0 for linear."""
-    return 1 if Method(method) is Method.SOFTMAX else 0
+    """The kernels' integer code of a method: 1 for softmax, 0 for linear."""
+    return int(Method(method) is Method.SOFTMAX)
 
 
 def apply_msda_method(attention_weights: Tensor, method: str | Method) -> Tensor:
-    """Normalize raw weights per ``method``; softmax runs over the joint ``L * P`` axis."""
-    method = Method(method)
-    if method is Method.LINEAR:
+    """The weights ``method`` makes of raw ``attention_weights``: as given (linear), or a
+    softmax over each (b, q, h)'s ``L * P`` points, flat ``(B, Q, H, L * P)`` or split
+    ``(B, Q, H, L, P)``."""
+    if Method(method) is Method.LINEAR:
         return attention_weights
-    if attention_weights.ndim == 5:  # noqa: PLR2004
-        flat = attention_weights.flatten(-2)
-        return torch.softmax(flat, -1).unflatten(-1, attention_weights.shape[-2:])
-    if attention_weights.ndim != 4:  # noqa: PLR2004
-        msg = (
-            f"attention weights must be (B, Q, G, L * K) or (B, Q, G, L, K); "
-            f"got {attention_weights.ndim} dimensions."
+    if attention_weights.ndim not in (4, 5):
+        raise ValueError(
+            f"attention weights are (B, Q, H, L * P) or (B, Q, H, L, P); got {attention_weights.ndim} "
+            f"dimensions"
         )
-        raise ValueError(msg)
-    return torch.softmax(attention_weights, -1)
+    flat = attention_weights.reshape(*attention_weights.shape[:3], -1)
+    return torch.softmax(flat, -1).reshape(attention_weights.shape)
 
 
 def resolve_msda_attn(attention_weights: Tensor, method: str | Method) -> tuple[Tensor, int]:
-    """``(weights, aggregate)``: softmax stays raw for an in-kernel softmax (code 1)."""
-    aggregate = msda_method_to_aggregate(method)
-    if aggregate == 1:
+    """``(weights, aggregate)`` for a kernel: softmax weights stay raw (the kernel applies
+    it, code 1); linear ones pass as given (code 0)."""
+    if msda_method_to_aggregate(method):
         return attention_weights, 1
     return apply_msda_method(attention_weights, method), 0
 
 
-def select_backend(context: MSDAContext) -> list[Backend | tuple[Backend, dict[str, Any]]]:
-    """Candidate backends for a ``backend=None`` call, in order.
-
-    GPU tensors (torch device type ``"cuda"``, which is HIP on ROCm) run the HIP
-    kernels, float64 included. CPU tensors ask for the eager backend, which this
-    build does not ship, so they raise :class:`~deformops_amd.core.errors.NoBackendError`
-    with that reason instead of silently running a CPU path.
-    """
-    if context.device.type != "cuda":
-        return [Backend.EAGER]
-    return [Backend.HIP]
+def select_backend(context: MSDAContext) -> list[Backend]:
+    """The policy for ``backend=None``: GPU tensors (device type ``"cuda"``, HIP on
+    ROCm) run the HIP kernels in every dtype, float64 included. The reference sends
+    CPU tensors to its eager backend, which this build does not ship, so they raise
+    ``NoBackendError`` saying so rather than falling back silently."""
+    return [Backend.HIP] if context.device.type == "cuda" else [Backend.EAGER]
 
 
-#: Keywords a backend consumes besides method/softmax (reference registry/msda.py:216-218).
-_CALL_OPTIONS: frozenset[str] = frozenset(
-    {"chunk_step", "num_points", "channels_per_thread", "threads_per_block", "fp32acc"}
-)
+#: Keywords a backend consumes besides method / softmax (reference registry/msda.py:216-218).
+_OPTIONS = frozenset({"chunk_step", "num_points", "channels_per_thread", "threads_per_block", "fp32acc"})
+#: Of those, the ones that configure a particular backend: such a call skips the
+#: public operator, whose schema cannot carry them.
+_BACKEND_OPTIONS = _OPTIONS - {"chunk_step"}
 
 
-def _checked_arguments(
-    level_start_index: Tensor | None,
-    sampling_locations: Tensor | None,
-    attention_weights: Tensor | None,
-    options: dict[str, Any],
-) -> tuple[Tensor, Tensor, Tensor]:
-    if level_start_index is None or sampling_locations is None or attention_weights is None:
-        msg = (
-            "msda takes (values, spatial_shapes, level_start_index, "
-            "sampling_locations, attention_weights) positionally"
-        )
-        raise TypeError(msg)
-    unknown = set(options) - _CALL_OPTIONS
+def _operands(args: tuple[Any, ...], options: dict[str, Any]) -> tuple[Tensor, ...]:
+    """The five positional tensors of a call; ``TypeError`` for a short call or an
+    unknown keyword."""
+    if len(args) != 5 or any(a is None for a in args):
+        raise TypeError("msda takes (value, spatial_shapes, level_start_index, sampling_locations, "
+                        f"attention_weights) positionally; got {len(args)} of them")
+    unknown = sorted(name for name in options if name not in _OPTIONS)
     if unknown:
-        msg = f"msda got unexpected keyword argument(s): {', '.join(sorted(unknown))}"
-        raise TypeError(msg)
-    return level_start_index, sampling_locations, attention_weights
+        raise TypeError(f"msda got unexpected keyword argument(s): {', '.join(unknown)}")
+    return args
 
 
-def _context_of(  # noqa: PLR0913
-    value: Tensor,
-    spatial_shapes: Tensor,
-    level_start_index: Tensor | None = None,
-    sampling_locations: Tensor | None = None,
-    attention_weights: Tensor | None = None,
-    *,
-    method: str | Method | None = None,
-    softmax: bool = False,
-    **options: Any,
-) -> MSDAContext:
-    level_start_index, sampling_locations, attention_weights = _checked_arguments(
-        level_start_index, sampling_locations, attention_weights, options
-    )
+def _context_of(*args: Any, method: str | Method | None = None, softmax: bool = False,
+                **options: Any) -> MSDAContext:
+    value, spatial_shapes, level_start_index, sampling_locations, attention_weights = _operands(args, options)
     check_msda_call(value, spatial_shapes, level_start_index, sampling_locations, attention_weights)
-    return MSDAContext.from_call(
-        value,
-        spatial_shapes,
-        sampling_locations,
-        attention_weights,
-        resolve_method(method, softmax=softmax),
-    )
+    return MSDAContext.from_call(value, spatial_shapes, sampling_locations, attention_weights,
+                                 resolve_method(method, softmax=softmax))
 
 
 def _msda_call(  # noqa: PLR0913
@@ -261,81 +222,61 @@ def _msda_call(  # noqa: PLR0913
 
     Notes
     -----
-    float32, float16, bfloat16 and float64 values run on the GPU. ``grad_value`` is
-    summed in fp32 (fp64 for float64) by the single owner of each element and
-    stored once in the value dtype; the backward uses no memory beyond the three
-    gradient tensors.
+    float32, float16, bfloat16 and float64 values run on the GPU, with fp32
+    attention * bilinear weights (fp64 for float64). ``grad_value`` is summed in
+    fp32 (fp64 for float64) by the single owner of each element and stored once;
+    the backward uses no memory beyond the three gradient tensors. Valid levels
+    that share positions of ``S`` sum their contributions into the shared
+    ``grad_value`` elements.
     """
     raise NotImplementedError
 
 
 msda = Registry("msda", context_of=_context_of, select=select_backend, describe=_msda_call)
 
-_PUBLIC_SCHEMA = (
-    "(Tensor value, Tensor spatial_shapes, Tensor level_start_index, "
-    "Tensor sampling_locations, Tensor attention_weights) -> Tensor"
-)
-_LEVEL_TABLE = "the spatial shapes and level start offsets"
-
-#: Keywords that override the policy, so such a call negotiates in Python.
-_OVERRIDE_OPTIONS: frozenset[str] = _CALL_OPTIONS - {"chunk_step"}
+_SCHEMA = ("(Tensor value, Tensor spatial_shapes, Tensor level_start_index, "
+           "Tensor sampling_locations, Tensor attention_weights) -> Tensor")
+_TABLES = {1: "spatial_shapes", 2: "level_start_index"}
 
 
 def _public_kernel(method: Method) -> Any:
-    def kernel(
-        value: Tensor,
-        spatial_shapes: Tensor,
-        level_start_index: Tensor,
-        sampling_locations: Tensor,
-        attention_weights: Tensor,
-    ) -> Tensor:
-        return msda.run_selected(
-            value,
-            spatial_shapes,
-            level_start_index,
-            sampling_locations,
-            attention_weights,
-            method=method,
-        )
+    def kernel(value: Tensor, spatial_shapes: Tensor, level_start_index: Tensor, sampling_locations: Tensor,
+               attention_weights: Tensor) -> Tensor:
+        return msda.run_selected(value, spatial_shapes, level_start_index, sampling_locations,
+                                 attention_weights, method=method)
 
     return kernel
 
 
-define_public_op("msda", _PUBLIC_SCHEMA, _public_kernel(Method.LINEAR), shared={1: _LEVEL_TABLE, 2: _LEVEL_TABLE})
-define_public_op(
-    "msda_softmax", _PUBLIC_SCHEMA, _public_kernel(Method.SOFTMAX), shared={1: _LEVEL_TABLE, 2: _LEVEL_TABLE}
-)
+_PUBLIC = {
+    Method.LINEAR: define_public_op("msda", _SCHEMA, _public_kernel(Method.LINEAR), fixed=_TABLES),
+    Method.SOFTMAX: define_public_op("msda_softmax", _SCHEMA, _public_kernel(Method.SOFTMAX), fixed=_TABLES),
+}
 
 
-def _route_selected(  # noqa: PLR0913
-    value: Tensor,
-    spatial_shapes: Tensor,
-    level_start_index: Tensor | None = None,
-    sampling_locations: Tensor | None = None,
-    attention_weights: Tensor | None = None,
-    *,
-    method: str | Method | None = None,
-    softmax: bool = False,
-    **options: Any,
-) -> Tensor:
-    """Run a ``backend=None`` call through ``deformops::msda[_softmax]``."""
-    if any(name in options for name in _OVERRIDE_OPTIONS):
-        return msda.run_selected(
-            value,
-            spatial_shapes,
-            level_start_index,
-            sampling_locations,
-            attention_weights,
-            method=method,
-            softmax=softmax,
-            **options,
-        )
-    level_start_index, sampling_locations, attention_weights = _checked_arguments(
-        level_start_index, sampling_locations, attention_weights, options
-    )
-    use_softmax = resolve_method(method, softmax=softmax) is Method.SOFTMAX
-    op = torch.ops.deformops.msda_softmax if use_softmax else torch.ops.deformops.msda
-    return op(value, spatial_shapes, level_start_index, sampling_locations, attention_weights)
+def _plain_eager(tensors: tuple[Tensor, ...]) -> bool:
+    """Whether nothing would observe the public operator: not compiling or tracing, no
+    dispatch or function mode (fake tensors, export), and real tensors that no
+    functorch transform (vmap, grad) wraps."""
+    if torch.compiler.is_compiling() or torch._C._len_torch_dispatch_stack():  # noqa: SLF001
+        return False
+    if torch._C._is_torch_function_mode_enabled():  # noqa: SLF001
+        return False
+    wrapped = torch._C._functorch.is_functorch_wrapped_tensor  # noqa: SLF001
+    return all(type(t) in (Tensor, torch.nn.Parameter) and not wrapped(t) for t in tensors)
+
+
+def _route_selected(*args: Any, method: str | Method | None = None, softmax: bool = False,
+                    **options: Any) -> Tensor:
+    """A ``backend=None`` call: the public operator, or the same work directly when
+    plain eager; backend options go to the selected backend."""
+    if any(name in _BACKEND_OPTIONS for name in options):
+        return msda.run_selected(*args, method=method, softmax=softmax, **options)
+    tensors = _operands(args, options)
+    chosen = resolve_method(method, softmax=softmax)
+    if _plain_eager(tensors):
+        return msda.run_selected(*tensors, method=chosen, **options)
+    return _PUBLIC[chosen](*tensors)
 
 
 msda.route_selected_calls(_route_selected)

@@ -245,3 +245,13 @@ def test_public_ops_carry_the_reference_schema():
             f"deformops::{name}(Tensor value, Tensor spatial_shapes, Tensor level_start_index, "
             "Tensor sampling_locations, Tensor attention_weights) -> Tensor"
         )
+
+
+def test_probe_library_exports_its_header():
+    """libmsda_probe.so (bench.py's row-gather probe) exports what include/msda_probe.h declares."""
+    header = HEADER.parent / "msda_probe.h"
+    declared = re.findall(r"^int\s+(msda_\w+)\(", header.read_text(), flags=re.M)
+    assert declared == ["msda_probe_row_gather"]
+    probe = ctypes.CDLL(str(Path(_lib.library_path()).parent / "libmsda_probe.so"))
+    for name in declared:
+        assert hasattr(probe, name)

@@ -180,3 +180,41 @@ def test_export_keeps_the_public_op_until_decomposed(device, name, method):
 @pytest.mark.parametrize(("name", "method"), CASES)
 def test_opcheck(device, name, method):
     torch.library.opcheck(op_of(name).default, make_operands(device, 2, 5, True))
+
+
+# vmap: the mapped axis folds into the batch axis (reference
+# registry/_vmap.py:19-82); the level tables may not be mapped.
+
+
+def test_vmap_over_level_tables_raises():
+    """Refused by the vmap rule itself, before any backend runs (so on the CPU too)."""
+    value, shapes, starts, loc, attn = make_operands("cpu", 2, 4, requires_grad=False)
+    stacked = torch.stack([shapes, shapes])
+    with pytest.raises(RuntimeError, match="spatial_shapes"):
+        torch.vmap(lambda s: msda(value, s, starts, loc, attn))(stacked)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(("name", "method"), CASES)
+def test_vmap_folds_into_the_batch(device, name, method):
+    """vmap over a stack of 3 batches (and over value alone, with locations and
+    weights shared) equals the per-batch calls, gradients included."""
+    value, shapes, starts, loc, attn = make_operands(device, 2, 5, requires_grad=False)
+    values = torch.stack([value, value * 2, value - 1])
+    locs = torch.stack([loc, loc.flip(1), loc * 0.5 + 0.2])
+    attns = torch.stack([attn, attn.flip(1), attn * 2])
+
+    def call(v, lo, a):
+        return msda(v, shapes, starts, lo, a, method=method)
+
+    mapped = torch.vmap(call)(values, locs, attns)
+    each = torch.stack([call(v, lo, a) for v, lo, a in zip(values, locs, attns)])
+    torch.testing.assert_close(mapped, each, rtol=1e-5, atol=1e-6)
+    shared = torch.vmap(call, in_dims=(0, None, None))(values, loc, attn)
+    torch.testing.assert_close(shared, torch.stack([call(v, loc, attn) for v in values]), rtol=1e-5, atol=1e-6)
+    leaves = [t.clone().requires_grad_(True) for t in (values, locs, attns)]
+    torch.vmap(call)(*leaves).square().sum().backward()
+    ref_leaves = [t.clone().requires_grad_(True) for t in (values, locs, attns)]
+    torch.stack([call(v, lo, a) for v, lo, a in zip(*ref_leaves)]).square().sum().backward()
+    for got, want in zip(leaves, ref_leaves):
+        torch.testing.assert_close(got.grad, want.grad, rtol=1e-4, atol=1e-5)
