@@ -360,6 +360,37 @@ def test_sixteen_bit_error_margin(device, cfg, dtype):
         assert max(errs.values()) <= bound, errs
 
 
+def test_atomic_grad_value_at_the_headline_loses_precision(device):
+    """The reason the default backward does not scatter grad_value with atomics, at
+    config 4 (one image): 16-bit atomics round every contribution into a 16-bit
+    sum (fan-in up to ~1,300 at the coarsest level), where the owners sum in fp32
+    and round once. Measured: norm-wise error against the oracle and the
+    directional bias |cos(mean error, gradient)| of grad_value (grad_out = 1, the
+    reference's tests/deformops/test_msda_bias.py), both paths, bf16 and fp32."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    base = make_workload(4, batch=1)
+    base.grad_output = torch.ones_like(base.grad_output)
+    value, shapes, starts, loc, attn = base.operands()
+    exact = oracle.backward(value, shapes, starts, loc, attn, base.grad_output, softmax=False)[0]
+    found = {}
+    for dtype in (BF16, F32):
+        w = base.to(device, dtype)
+        rounded = [t.double().cpu() for t in (w.value, w.sampling_locations, w.attention_weights)]
+        expected = oracle.backward(rounded[0], shapes, starts, rounded[1], rounded[2], base.grad_output,
+                                   softmax=False)[0]
+        for name, flags in (("owner", 0), ("atomic", _lib.FLAG_GRAD_VALUE_ATOMIC)):
+            gv = abi_backward(w, flags)[0].double().cpu()
+            err = gv - expected
+            cos = (err * exact).sum().item() / (err.norm().item() * exact.norm().item() + 1e-30)
+            found[(dtype, name)] = (rel_err(gv, expected), cos)
+    print("config 4, one image, grad_value (norm-wise error, bias cos):",
+          {f"{str(d).split('.')[-1]} {n}": (f"{e:.2e}", f"{c:+.3f}") for (d, n), (e, c) in found.items()})
+    assert found[(BF16, "owner")][0] <= 2.0**-8
+    assert found[(BF16, "atomic")][0] > 4 * found[(BF16, "owner")][0]
+    assert found[(F32, "owner")][0] <= BWD_TOL[F32] and found[(F32, "atomic")][0] <= BWD_TOL[F32]
+
+
 # Overlapping level tables: two valid levels that share positions of S. The forward
 # samples each level as given; the backward sums every level's contribution into a
 # shared grad_value element, as the oracle and the reference's eager path do (its
