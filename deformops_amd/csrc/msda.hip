@@ -1859,17 +1859,20 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
 // back: A (position-major weight tiles) with ds_read_b128, B (grad_out, K-major)
 // with two ds_read_b64_tr_b16 per 16 channels.
 //
-// Every value dtype runs v_mfma_f32_16x16x32_bf16 on operands split into two bf16
-// parts, x = hi + lo + e: hi is x rounded to bf16 (nearest even) and lo the rest
-// rounded again, so |e| <= 2^-16 |x|.
-//   - W (fp32 attention * bilinear) is split for every dtype: two weight tiles per
-//     sub-tile, W_hi and W_lo.
-//   - G is exact in bf16 for bf16 values. f16 and float rows are split too, into
-//     two staged row buffers; f16's 11 significant bits fit hi + lo exactly.
+// Operands are split into two 16-bit parts, x = hi + lo + e: hi is x rounded to the
+// operand type (nearest even) and lo the rest rounded again.
+//   - bf16 values: v_mfma_f32_16x16x32_bf16, W (the fp32 attention * bilinear weight)
+//     split into bf16 parts (|e| <= 2^-16 |W|: two weight tiles per sub-tile, W_hi
+//     and W_lo), G exact in bf16.
+//   - f16 values: v_mfma_f32_16x16x32_f16, W split into f16 parts (|e| <= 2^-22 |W|
+//     while W_lo stays in f16's normal range, else |e| <= 2^-25), G exact in f16. W
+//     never exceeds the f16 attention weight it scales, so W_hi cannot overflow.
+//   - float values: v_mfma_f32_16x16x32_bf16 on bf16 parts of W and of G (two
+//     staged row buffers, G_hi and G_lo).
 //   - Per sub-tile, 16 channels and K-step the MFMAs add W_hi G_hi + W_lo G_hi, and
 //     W_hi G_lo when G is split. Products are exact and sums fp32, so a product's
-//     relative error is at most 2^-16 (bf16), 2^-15 (f16: the dropped W_lo G_lo) and
-//     3 * 2^-16 (float: W_lo G_lo and the two splits).
+//     relative error is at most 2^-16 (bf16), 2^-22 (f16, normal range) and
+//     3 * 2^-16 (float: the dropped W_lo G_lo and the two splits).
 // Waves do not wait for each other inside a task; the loads of the next K-block (and
 // the entries of the one after) are in flight while a K-block computes. A split
 // task's four partial sums meet in LDS at its end and wave w writes sub-tile w.
@@ -1887,6 +1890,7 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
 // non-finite value is zero, so an infinite product stays infinite.
 
 typedef __bf16 bf16x8_v __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
 typedef float f32x4_v __attribute__((ext_vector_type(4)));
 typedef short i16x4_v __attribute__((ext_vector_type(4)));
 
@@ -1896,17 +1900,23 @@ constexpr int kMfmaK = 64;        // candidates per K-block: one per lane, two M
 constexpr int kMfmaKStep = 32;    // the MFMA's K
 constexpr int kMfmaMaxNb = 4;     // 16-channel column blocks: D <= 64
 
-// One 16 x 32 bf16 weight tile (16 positions, one K-step of candidates); a K-step
-// has four sub-tiles of hi tiles, then four of lo tiles. A staged grad_out row holds
-// 16 nb bf16 channels.
+// One 16 x 32 weight tile of 16-bit parts (16 positions, one K-step of candidates);
+// a K-step has four sub-tiles of hi tiles, then four of lo tiles. A staged grad_out
+// row holds 16 nb 16-bit channels.
 constexpr int kMfmaWBytes = 16 * kMfmaKStep * 2;
 constexpr int kMfmaLoTiles = 4 * kMfmaWBytes;  // offset of the lo tiles
 constexpr int mfma_row_bytes(int nb) { return 16 * nb * 2; }
-// Whether grad_out rows of a value dtype are split into hi and lo (f16 and float).
-constexpr bool mfma_split_rows(int es, bool bf16) { return !(es == 2 && bf16); }
+// The MFMA operand type of a value dtype: f16 for f16 values, bf16 otherwise.
+template <typename T> constexpr bool mfma_f16_operands() { return std::is_same_v<T, f16_t>; }
 
-__device__ inline f32x4_v mfma_bf16(bf16x8_v a, bf16x8_v b, f32x4_v c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+template <bool F16>
+__device__ inline f32x4_v mfma_16x16x32(const u32x4_v& a, const u32x4_v& b, f32x4_v c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, a), __builtin_bit_cast(f16x8_v, b), c,
+                                                  0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), __builtin_bit_cast(bf16x8_v, b),
+                                                   c, 0, 0, 0);
 }
 
 // The bf16 parts of x (see above); lo is zero for a non-finite x.
@@ -1914,6 +1924,13 @@ __device__ inline void split_bf16(float x, uint16_t* hi, uint16_t* lo) {
   const __bf16 h = static_cast<__bf16>(x);
   *hi = __builtin_bit_cast(uint16_t, h);
   const __bf16 r = static_cast<__bf16>(x - static_cast<float>(h));
+  *lo = __builtin_isfinite(x) ? __builtin_bit_cast(uint16_t, r) : uint16_t(0);
+}
+// The f16 parts of x; lo is zero for a non-finite x.
+__device__ inline void split_f16(float x, uint16_t* hi, uint16_t* lo) {
+  const _Float16 h = static_cast<_Float16>(x);
+  *hi = __builtin_bit_cast(uint16_t, h);
+  const _Float16 r = static_cast<_Float16>(x - static_cast<float>(h));
   *lo = __builtin_isfinite(x) ? __builtin_bit_cast(uint16_t, r) : uint16_t(0);
 }
 // Two floats to packed (hi, lo) bf16 pairs, element 0 in the low halves.
@@ -2060,8 +2077,8 @@ __device__ inline void mfma_load_rows(const MfmaTile& t, uint32_t e, int lane, M
 
 // One K-block of one wave, in two parts. Part A: the candidate's corners (as LDS
 // byte offsets of their weights in the hi weight tiles, -1 outside the tile, and the
-// weights' bf16 parts), and the block's 64 grad_out rows into LDS as bf16 (hi and
-// lo buffers when split), after which the row registers are free for the next
+// weights' 16-bit parts), and the block's 64 grad_out rows into LDS as 16-bit
+// operands (hi and lo buffers when split), after which the row registers are free for the next
 // block's loads. Part B: per MFMA K-step (the candidates of lanes 0-31, then 32-63)
 // scatter the corner weights into the weight tiles, run the sub-tiles' MFMAs, and
 // clear the scattered entries again. The tiles are zeroed once (mfma_zero_tiles) and
@@ -2073,23 +2090,12 @@ struct MfmaCorners {
   uint16_t hi[4], lo[4];
 };
 
-// A staged 16-byte piece of a grad_out row as bf16: copied (bf16), or split into
-// hi and lo parts (f16: 8 channels, 16 bytes each; float: 4 channels, 8 bytes each).
+// A staged 16-byte piece of a grad_out row: copied (bf16, f16), or split into bf16
+// hi and lo parts (float: 4 channels, 8 bytes each).
 template <typename T>
 __device__ inline void mfma_stage_piece(const u32x4_v& v, unsigned char* hi, unsigned char* lo) {
-  if constexpr (std::is_same_v<T, bf16_t>) {
+  if constexpr (sizeof(T) == 2) {
     *reinterpret_cast<u32x4_v*>(hi) = v;
-  } else if constexpr (std::is_same_v<T, f16_t>) {
-    u32x4_v h, l;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t hw, lw;
-      split_bf16_pair(f16_bits(v[i] & 0xffffu), f16_bits(v[i] >> 16), &hw, &lw);
-      h[i] = hw;
-      l[i] = lw;
-    }
-    *reinterpret_cast<u32x4_v*>(hi) = h;
-    *reinterpret_cast<u32x4_v*>(lo) = l;
   } else {
     u32x2_v h, l;
 #pragma unroll
@@ -2111,7 +2117,7 @@ __device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, 
   constexpr int ES = int(sizeof(T));
   constexpr int kPieces = mfma_pieces<T, NB>();
   constexpr int kRowBytes = mfma_row_bytes(NB);
-  constexpr int kStagedPiece = 16 * 2 / ES;  // bf16 bytes a 16-byte piece becomes
+  constexpr int kStagedPiece = 16 * 2 / ES;  // staged bytes a 16-byte piece becomes
   constexpr size_t kLoRows = size_t(kMfmaK) * kRowBytes;
   const int kc = lane & (kMfmaKStep - 1);
   const uint32_t c = kb * kMfmaK + uint32_t(lane);
@@ -2145,7 +2151,10 @@ __device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, 
       if (m[k] && y >= 0 && x >= 0 && t.r0 + y < t.r1 && t.c0 + x < t.c1) {
         const int pos = (y & 3) * 4 + (x & 3);
         cr.o[k] = ((y >> 2) * 2 + (x >> 2)) * kMfmaWBytes + pos * (2 * kMfmaKStep) + kc * 2;
-        split_bf16(wb[k] * a, &cr.hi[k], &cr.lo[k]);
+        if constexpr (mfma_f16_operands<T>())
+          split_f16(wb[k] * a, &cr.hi[k], &cr.lo[k]);
+        else
+          split_bf16(wb[k] * a, &cr.hi[k], &cr.lo[k]);
       }
     }
   }
@@ -2165,7 +2174,8 @@ __device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, 
 template <typename T, int NB, bool TAIL = false>
 __device__ inline void mfma_kblock_b(const MfmaCorners& cr, int lane, const unsigned char* gst, unsigned char* wt,
                                      f32x4_v (&acc)[4][NB], int ksteps = 2) {
-  constexpr bool kSplit = !std::is_same_v<T, bf16_t>;
+  constexpr bool kSplit = sizeof(T) == 4;
+  constexpr bool kF16 = mfma_f16_operands<T>();
   constexpr int kRowBytes = mfma_row_bytes(NB);
   constexpr size_t kLoRows = size_t(kMfmaK) * kRowBytes;
   const int half = lane >> 5;
@@ -2184,29 +2194,28 @@ __device__ inline void mfma_kblock_b(const MfmaCorners& cr, int lane, const unsi
         }
     }
     wave_lds_order();
-    bf16x8_v bh[NB], bl[NB];
+    u32x4_v bh[NB], bl[NB];
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const unsigned char* src =
           gst + (kMfmaKStep * ks + 8 * g16 + i16 / 4) * kRowBytes + (16 * nb + 4 * (i16 & 3)) * 2;
-      bh[nb] = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(lds_read_tr16(src), lds_read_tr16(src + 4 * kRowBytes),
-                                                                     0, 1, 2, 3, 4, 5, 6, 7));
+      bh[nb] = __builtin_bit_cast(u32x4_v, __builtin_shufflevector(lds_read_tr16(src), lds_read_tr16(src + 4 * kRowBytes),
+                                                                    0, 1, 2, 3, 4, 5, 6, 7));
       if constexpr (kSplit)
-        bl[nb] = __builtin_bit_cast(bf16x8_v, __builtin_shufflevector(lds_read_tr16(src + kLoRows),
-                                                                       lds_read_tr16(src + kLoRows + 4 * kRowBytes),
-                                                                       0, 1, 2, 3, 4, 5, 6, 7));
+        bl[nb] = __builtin_bit_cast(u32x4_v, __builtin_shufflevector(lds_read_tr16(src + kLoRows),
+                                                                      lds_read_tr16(src + kLoRows + 4 * kRowBytes),
+                                                                      0, 1, 2, 3, 4, 5, 6, 7));
     }
     const int aoff = i16 * (2 * kMfmaKStep) + g16 * 16;
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
-      const bf16x8_v ah = __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const u32x4_v*>(wt + st * kMfmaWBytes + aoff));
-      const bf16x8_v al =
-          __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const u32x4_v*>(wt + kMfmaLoTiles + st * kMfmaWBytes + aoff));
+      const u32x4_v ah = *reinterpret_cast<const u32x4_v*>(wt + st * kMfmaWBytes + aoff);
+      const u32x4_v al = *reinterpret_cast<const u32x4_v*>(wt + kMfmaLoTiles + st * kMfmaWBytes + aoff);
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        if constexpr (kSplit) acc[st][nb] = mfma_bf16(ah, bl[nb], acc[st][nb]);
-        acc[st][nb] = mfma_bf16(al, bh[nb], acc[st][nb]);
-        acc[st][nb] = mfma_bf16(ah, bh[nb], acc[st][nb]);
+        if constexpr (kSplit) acc[st][nb] = mfma_16x16x32<false>(ah, bl[nb], acc[st][nb]);
+        acc[st][nb] = mfma_16x16x32<kF16>(al, bh[nb], acc[st][nb]);
+        acc[st][nb] = mfma_16x16x32<kF16>(ah, bh[nb], acc[st][nb]);
       }
     }
     wave_lds_order();
@@ -2395,7 +2404,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
   at = (at + 15) & ~size_t(15);
   int64_t* total = reinterpret_cast<int64_t*>(smem + at);  // [0]: tiles, [1]: the fetched task
   at += 16;
-  constexpr bool kSplit = !std::is_same_v<T, bf16_t>;
+  constexpr bool kSplit = sizeof(T) == 4;
   constexpr size_t kRowsBytes = size_t(kMfmaK) * size_t(mfma_row_bytes(NB)) * (kSplit ? 2 : 1);
   constexpr size_t kWaveBytes = std::max(kRowsBytes + 8 * size_t(kMfmaWBytes), size_t(4 * NB * kWave * 16));
   unsigned char* region0 = smem + at;
@@ -3095,10 +3104,10 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   const int64_t ls = elem_size(loc_dtype);
   const int64_t per_image = Q * H * std::max(L * P * 2 * ls, D * es);  // 32-bit offsets inside an image
   const bool mfma_sure = 4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc;
-  // The matrix-core kernel's LDS: per wave the staged rows (split for f16 and float)
+  // The matrix-core kernel's LDS: per wave the staged rows (split for float)
   // and the weight tiles, plus its queue's prefix table of (pair, level) entries: at
   // most 16 x 16 regions per image, an eighth of the (image, region) pairs per queue.
-  const bool mfma_split = dtype != MSDA_BF16;
+  const bool mfma_split = dtype == MSDA_F32;
   const int mfma_table = int(std::min<int64_t>(kMfmaTable, ((B * 256 + kXcds - 1) / kXcds) * L));
   const size_t mfma_lds = mfma_lds_bytes(L, D, mfma_split) + sizeof(int) * size_t(2 * mfma_table + 1);
   const bool mfma_likely = 4 * mfma_tiles_estimate + kQueueInts <= bg.keys_alloc && bg.cap >= 64;

@@ -105,8 +105,9 @@ int msda_forward(const void* value, int value_dtype,
  * MSDA_ACCUMULATE_GRAD_VALUE the previous contents are added to that sum. No
  * atomics touch grad_value, it needs no zero-fill, and there is no float32 copy.
  * For bf16, f16 and float values the owner sums on the matrix cores with each
- * weight * grad_out product formed from 16-bit-significand parts (relative error
- * at most 2^-16 for bf16, 2^-15 for f16, 3 * 2^-16 for float; see msda.hip).
+ * weight * grad_out product formed from 16-bit parts (relative error at most 2^-16
+ * for bf16, 2^-22 for f16 while the weight's low part is a normal f16 number, and
+ * 3 * 2^-16 for float; see msda.hip).
  * The order in which an element's contributions are summed follows the order the
  * bucket sort gives the samples, which depends on the order of its LDS atomics
  * across waves; so the last bits of grad_value may vary between runs. The other two
