@@ -20,6 +20,7 @@ by its one owner and stored once. ``chunk_step``, ``channels_per_thread`` and
 
 from __future__ import annotations
 
+import contextlib
 from typing import Any
 
 import torch
@@ -282,9 +283,9 @@ def forward(
         num_points = int(sampling_locations.shape[4])
     shapes, starts = _index_tables(spatial_shapes, level_start_index)
     loc = sampling_locations.to(_location_dtype(value.dtype, sampling_locations.dtype))
-    with torch.autocast("cuda", enabled=False):
-        operands = (value.contiguous(), shapes, starts, loc.contiguous(),
-                    attention_weights.to(value.dtype).contiguous())
+    operands = (value.contiguous(), shapes, starts, loc.contiguous(), attention_weights.to(value.dtype).contiguous())
+    # The kernels take the operands in their own dtypes: no autocast inside.
+    with torch.autocast("cuda", enabled=False) if torch.is_autocast_enabled("cuda") else contextlib.nullcontext():
         if _plain_eager(*operands):
             _check_points(operands[3], num_points)
             return _EagerMSDA.apply(*operands, softmax)
@@ -293,7 +294,7 @@ def forward(
 
 
 def _channels_per_lane(dtype: torch.dtype, head_dim: int) -> int:
-    cv = 16 // torch.empty((), dtype=dtype).element_size()
+    cv = 16 // dtype.itemsize
     while cv > 1 and head_dim % cv:
         cv //= 2
     return cv
@@ -325,7 +326,7 @@ def supports_context(context: MSDAContext) -> bool:
         return False
     f64 = context.dtype == torch.float64
     staged = 48 if f64 else 32
-    value_bytes = torch.empty((), dtype=context.dtype).element_size()
+    value_bytes = context.dtype.itemsize
     loc_bytes = 8 if f64 else 4
 
     def align16(n: int) -> int:

@@ -144,6 +144,9 @@ class Registry:
         self._route: Callable[..., Any] | None = None
         self._adapters_ready = False
         self._lock = threading.Lock()
+        # Choices that passed over no backend, per context: a repeated call skips the
+        # policy and the support predicates. Emptied whenever the table changes.
+        self._chosen: dict[Any, Resolution] = {}
         if describe is not None:
             self.__doc__ = describe.__doc__
             self.__signature__ = inspect.signature(describe)
@@ -163,11 +166,13 @@ class Registry:
         _require_backend(backend, allow_none=False)
         self._entries[backend] = _Entry(op_handle, supports, load)
         self._absent.pop(backend, None)
+        self._chosen.clear()
 
     def mark_unavailable(self, backend: Backend, reason: str) -> None:
         """Record why ``backend`` is not registered; error messages quote it."""
         if backend not in self._entries:
             self._absent[backend] = reason
+            self._chosen.clear()
 
     def route_selected_calls(self, route: Callable[..., Any]) -> None:
         """Send ``backend=None`` calls through ``route`` (the public operator)."""
@@ -241,6 +246,9 @@ class Registry:
         return None
 
     def _choose(self, context: Any) -> Resolution:
+        known = self._chosen.get(context)
+        if known is not None:
+            return known
         rejected: list[tuple[Backend, str]] = []
         for backend, options in _candidates(self._select(context)):
             reason = self._refusal(backend, context)
@@ -252,7 +260,10 @@ class Registry:
                 warnings.warn(f"{self.name} runs on {backend.value!r}, passing over {passed}. Set "
                               f"{FALLBACK_WARNINGS_ENV_VAR}=0 to silence this.", BackendFallbackWarning,
                               stacklevel=4)
-            return Resolution(backend, options, tuple(rejected))
+            resolution = Resolution(backend, options, tuple(rejected))
+            if not rejected:
+                self._chosen[context] = resolution
+            return resolution
         tried = "; ".join(f"{b.value!r}: {why}" for b, why in rejected) or "none"
         raise NoBackendError(f"No backend can run this {self.name} call ({context!r}). Candidates: {tried}.")
 
