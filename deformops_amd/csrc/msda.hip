@@ -2337,7 +2337,7 @@ constexpr int mfma_blocks_per_cu(int nb, int es) {
   return es == 4 ? (nb == 1 ? 3 : 2) : (nb == 1 ? 4 : nb == 2 ? 3 : 2);
 }
 
-constexpr int kMfmaMaxRegions = 16;  // regions per axis at most
+constexpr int kMfmaMaxRegions = 8;   // regions per axis at most
 constexpr int kMfmaTable = 1024;      // entries of a queue's prefix table at most
 constexpr int kMfmaMaxChunk = 8;      // tasks a workgroup takes from its queue at once, at most
 
