@@ -2438,7 +2438,8 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
   const bool stats_ok = SOFTMAX && softmax_stats_fit<float>(p, bg, 4 * ntiles, buckets);
   if (tid == 0) {
     order_levels(p, levels, lt, order, rank_base);
-    // R x R regions, R the power of two nearest the finest level's tile count, at most 16.
+    // R x R regions, R the power of two nearest the finest level's tile count, at most
+    // kMfmaMaxRegions.
     int mt = 1;
     for (int i = 0; i < p.L; ++i) mt = max(mt, max(lt[i].ntx, lt[i].nty));
     int r = 1;
@@ -3106,9 +3107,10 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   const bool mfma_sure = 4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc;
   // The matrix-core kernel's LDS: per wave the staged rows (split for float)
   // and the weight tiles, plus its queue's prefix table of (pair, level) entries: at
-  // most 16 x 16 regions per image, an eighth of the (image, region) pairs per queue.
+  // most kMfmaMaxRegions^2 regions per image, an eighth of the (image, region) pairs per queue.
   const bool mfma_split = dtype == MSDA_F32;
-  const int mfma_table = int(std::min<int64_t>(kMfmaTable, ((B * 256 + kXcds - 1) / kXcds) * L));
+  const int mfma_table = int(std::min<int64_t>(
+      kMfmaTable, ((B * kMfmaMaxRegions * kMfmaMaxRegions + kXcds - 1) / kXcds) * L));
   const size_t mfma_lds = mfma_lds_bytes(L, D, mfma_split) + sizeof(int) * size_t(2 * mfma_table + 1);
   const bool mfma_likely = 4 * mfma_tiles_estimate + kQueueInts <= bg.keys_alloc && bg.cap >= 64;
   bool mfma_ok = (dtype == MSDA_BF16 || dtype == MSDA_F16 || dtype == MSDA_F32) && D % 16 == 0 &&
