@@ -93,11 +93,64 @@ def _check_points(loc: Tensor, K: int) -> None:  # noqa: N803
         raise ValueError(msg)
 
 
-def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+def _on_device(device: torch.device) -> Any:
+    """The device's context when it is not the current one (the library launches on
+    the current device)."""
+    return contextlib.nullcontext() if device.index == torch.cuda.current_device() else torch.cuda.device(device)
 
 
-# Device kernels.
+# Device kernels. The launch functions take operands as _forward_impl and
+# _backward_impl normalize them (contiguous, level tables in a kernel index dtype,
+# locations in a kernel location dtype, weights in the value dtype).
+
+
+def _launch_forward(value: Tensor, shapes: Tensor, starts: Tensor, loc: Tensor, attn: Tensor, *,
+                    softmax: bool) -> Tensor:
+    B, S, H, D, Q, L, P = _sizes(value, shapes, loc)
+    out = torch.empty((B, Q, H * D), dtype=value.dtype, device=value.device)
+    lib = _lib.load()
+    with _on_device(value.device):
+        status = lib.forward(
+            value.data_ptr(), _lib.DTYPE_CODES[value.dtype],
+            shapes.data_ptr(), starts.data_ptr(), _lib.INDEX_CODES[shapes.dtype],
+            loc.data_ptr(), _lib.DTYPE_CODES[loc.dtype],
+            attn.data_ptr(), out.data_ptr(),
+            B, S, H, D, Q, L, P,
+            _lib.FLAG_SOFTMAX if softmax else 0,
+            torch._C._cuda_getCurrentRawStream(value.device.index),  # noqa: SLF001
+        )
+    lib.check(status)
+    return out
+
+
+def _launch_backward(value: Tensor, shapes: Tensor, starts: Tensor, loc: Tensor, attn: Tensor,
+                     grad_output: Tensor, *, softmax: bool) -> tuple[Tensor, Tensor, Tensor]:
+    B, S, H, D, Q, L, P = _sizes(value, shapes, loc)
+    grad_c = grad_output.to(value.dtype).contiguous()
+    grad_value = torch.empty_like(value)
+    grad_loc = torch.empty_like(loc)
+    grad_attn = torch.empty_like(attn)
+    lib = _lib.load()
+    with _on_device(value.device):
+        status = lib.backward(
+            value.data_ptr(), _lib.DTYPE_CODES[value.dtype],
+            shapes.data_ptr(), starts.data_ptr(), _lib.INDEX_CODES[shapes.dtype],
+            loc.data_ptr(), _lib.DTYPE_CODES[loc.dtype],
+            attn.data_ptr(), grad_c.data_ptr(),
+            grad_value.data_ptr(), grad_loc.data_ptr(), grad_attn.data_ptr(),
+            B, S, H, D, Q, L, P,
+            _lib.FLAG_SOFTMAX if softmax else 0,
+            torch._C._cuda_getCurrentRawStream(value.device.index),  # noqa: SLF001
+        )
+    lib.check(status)
+    return grad_value, grad_loc, grad_attn
+
+
+def _normalized(value: Tensor, spatial_shapes: Tensor, level_start_index: Tensor, loc: Tensor,
+                attn: Tensor) -> tuple[Tensor, ...]:
+    shapes, starts = _index_tables(spatial_shapes, level_start_index)
+    return (value.contiguous(), shapes, starts, loc.to(_location_dtype(value.dtype, loc.dtype)).contiguous(),
+            attn.to(value.dtype).contiguous())
 
 
 def _forward_impl(
@@ -105,25 +158,7 @@ def _forward_impl(
     attn: Tensor, K: int, *, softmax: bool,  # noqa: N803
 ) -> Tensor:
     _check_points(loc, K)
-    B, S, H, D, Q, L, P = _sizes(value, spatial_shapes, loc)
-    value_c = value.contiguous()
-    shapes, starts = _index_tables(spatial_shapes, level_start_index)
-    loc_c = loc.to(_location_dtype(value.dtype, loc.dtype)).contiguous()
-    attn_c = attn.to(value.dtype).contiguous()
-    out = torch.empty((B, Q, H * D), dtype=value.dtype, device=value.device)
-    lib = _lib.load()
-    with torch.cuda.device(value.device):
-        status = lib.forward(
-            value_c.data_ptr(), _lib.DTYPE_CODES[value.dtype],
-            shapes.data_ptr(), starts.data_ptr(), _lib.INDEX_CODES[shapes.dtype],
-            loc_c.data_ptr(), _lib.DTYPE_CODES[loc_c.dtype],
-            attn_c.data_ptr(), out.data_ptr(),
-            B, S, H, D, Q, L, P,
-            _lib.FLAG_SOFTMAX if softmax else 0,
-            _stream(value.device),
-        )
-    lib.check(status)
-    return out
+    return _launch_forward(*_normalized(value, spatial_shapes, level_start_index, loc, attn), softmax=softmax)
 
 
 def _backward_impl(
@@ -131,28 +166,8 @@ def _backward_impl(
     attn: Tensor, grad_output: Tensor, K: int, *, softmax: bool,  # noqa: N803
 ) -> tuple[Tensor, Tensor, Tensor]:
     _check_points(loc, K)
-    B, S, H, D, Q, L, P = _sizes(value, spatial_shapes, loc)
-    value_c = value.contiguous()
-    shapes, starts = _index_tables(spatial_shapes, level_start_index)
-    loc_c = loc.to(_location_dtype(value.dtype, loc.dtype)).contiguous()
-    attn_c = attn.to(value.dtype).contiguous()
-    grad_c = grad_output.to(value.dtype).contiguous()
-    grad_value = torch.empty_like(value_c)
-    grad_loc = torch.empty_like(loc_c)
-    grad_attn = torch.empty_like(attn_c)
-    lib = _lib.load()
-    with torch.cuda.device(value.device):
-        status = lib.backward(
-            value_c.data_ptr(), _lib.DTYPE_CODES[value.dtype],
-            shapes.data_ptr(), starts.data_ptr(), _lib.INDEX_CODES[shapes.dtype],
-            loc_c.data_ptr(), _lib.DTYPE_CODES[loc_c.dtype],
-            attn_c.data_ptr(), grad_c.data_ptr(),
-            grad_value.data_ptr(), grad_loc.data_ptr(), grad_attn.data_ptr(),
-            B, S, H, D, Q, L, P,
-            _lib.FLAG_SOFTMAX if softmax else 0,
-            _stream(value.device),
-        )
-    lib.check(status)
+    operands = _normalized(value, spatial_shapes, level_start_index, loc, attn)
+    grad_value, grad_loc, grad_attn = _launch_backward(*operands, grad_output, softmax=softmax)
     return grad_value, grad_loc.to(loc.dtype), grad_attn.to(attn.dtype)
 
 
@@ -225,17 +240,16 @@ class _EagerMSDA(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, value, spatial_shapes, level_start_index, loc, attn, softmax):  # noqa: ANN001, ANN205, PLR0913
+        # The operands come normalized from `forward` below.
         ctx.save_for_backward(value, spatial_shapes, level_start_index, loc, attn)
         ctx.softmax = softmax
-        return _forward_impl(value, spatial_shapes, level_start_index, loc, attn, int(loc.shape[4]),
-                             softmax=softmax)
+        return _launch_forward(value, spatial_shapes, level_start_index, loc, attn, softmax=softmax)
 
     @staticmethod
     def backward(ctx, grad_output):  # noqa: ANN001, ANN205
         value, spatial_shapes, level_start_index, loc, attn = ctx.saved_tensors
-        grad_value, grad_loc, grad_attn = _backward_impl(
-            value, spatial_shapes, level_start_index, loc, attn, grad_output, int(loc.shape[4]),
-            softmax=ctx.softmax,
+        grad_value, grad_loc, grad_attn = _launch_backward(
+            value, spatial_shapes, level_start_index, loc, attn, grad_output, softmax=ctx.softmax
         )
         return grad_value, None, None, grad_loc, grad_attn, None
 
@@ -281,9 +295,7 @@ def forward(
         raise RuntimeError(msg)
     if num_points is None:
         num_points = int(sampling_locations.shape[4])
-    shapes, starts = _index_tables(spatial_shapes, level_start_index)
-    loc = sampling_locations.to(_location_dtype(value.dtype, sampling_locations.dtype))
-    operands = (value.contiguous(), shapes, starts, loc.contiguous(), attention_weights.to(value.dtype).contiguous())
+    operands = _normalized(value, spatial_shapes, level_start_index, sampling_locations, attention_weights)
     # The kernels take the operands in their own dtypes: no autocast inside.
     with torch.autocast("cuda", enabled=False) if torch.is_autocast_enabled("cuda") else contextlib.nullcontext():
         if _plain_eager(*operands):
