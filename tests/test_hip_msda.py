@@ -360,6 +360,24 @@ def test_sixteen_bit_error_margin(device, cfg, dtype):
         assert max(errs.values()) <= bound, errs
 
 
+@pytest.mark.parametrize("dtype", [BF16, F32], ids=["bf16", "f32"])
+def test_grad_value_at_an_unaligned_offset(device, dtype):
+    """A grad_value one element past its allocation's alignment (a caller's offset
+    view): the grouped sort cannot park its 8- or 16-byte key words there, the
+    matrix-core owner cannot store 16-byte rows and the sample kernel takes one
+    channel per lane, so the call runs the per-sample sort and the VALU owner.
+    Every gradient still matches the oracle."""
+    w = make_workload(0, queries=200).to(device, dtype)
+    value, shapes, starts, loc, attn = w.operands()
+    flat = torch.empty(value.numel() + 1, dtype=dtype, device=device)
+    shifted = flat[1:].view(value.shape)
+    assert shifted.data_ptr() % 16 == value.element_size()
+    gv, gl, ga = abi_backward(w, 0, grad_value=shifted)
+    expected = oracle.backward(value, shapes, starts, loc, attn, w.grad_output, softmax=False)
+    for got, want in zip((gv, gl, ga), expected):
+        assert rel_err(got, want) <= BWD_TOL[dtype]
+
+
 def test_atomic_grad_value_at_the_headline_loses_precision(device):
     """The reason the default backward does not scatter grad_value with atomics, at
     config 4 (one image): 16-bit atomics round every contribution into a 16-bit
