@@ -8,12 +8,13 @@ Interface of the reference's registry (sources/deformops/registry/_dispatch.py:
 policy that is registered, supports the call and loads its kernels; a raw string
 for ``backend`` is a ``TypeError``.
 
-This build ships one backend, the HIP kernels, so the table is small and the
-choice needs no memo: a policy names one or two candidates, and checking them is a
-dictionary lookup, a predicate on the call's context and an already-loaded
-library. ``Backend.CUDA`` is an alias of ``Backend.HIP``, so code written for the
-reference's CUDA backend runs the HIP kernels; ``TRITON`` and ``EAGER`` exist so
-that such code imports, and asking for them says why they are absent.
+This build ships two backends: the HIP kernels for GPU tensors and, for CPU
+tensors only, torch operators (``EAGER``). So the table is small and the choice
+needs little: a policy names one candidate, and checking it is a dictionary
+lookup, a predicate on the call's context and an already-loaded library.
+``Backend.CUDA`` is an alias of ``Backend.HIP``, so code written for the
+reference's CUDA backend runs the HIP kernels; ``TRITON`` exists so that such code
+imports, and asking for it says why it is absent.
 """
 
 from __future__ import annotations
@@ -38,8 +39,8 @@ FALLBACK_WARNINGS_ENV_VAR = "DEFORMOPS_FALLBACK_WARNINGS"
 
 class Backend(str, Enum):
     """Compute backends. ``CUDA`` is an alias of ``HIP`` (torch's device type on ROCm is
-    ``"cuda"``, and ``Backend("cuda")`` is ``HIP``); ``TRITON`` and ``EAGER`` are never
-    registered in this build."""
+    ``"cuda"``, and ``Backend("cuda")`` is ``HIP``); ``EAGER`` takes CPU tensors only,
+    and ``TRITON`` is never registered in this build."""
 
     HIP = "hip"
     CUDA = "hip"
@@ -82,11 +83,14 @@ class _Entry:
 
 
 #: Packages that hold each backend's adapter module (``<package>.<operator>``).
-_ADAPTERS: dict[Backend, str] = {Backend.HIP: "deformops_amd.backends.hip"}
+_ADAPTERS: dict[Backend, str] = {
+    Backend.HIP: "deformops_amd.backends.hip",
+    Backend.EAGER: "deformops_amd.backends.eager",
+}
 
 _NOT_BUILT = (
-    "it is not part of this build, which runs MSDA only on AMD GPUs through its HIP "
-    "kernels (Backend.HIP)"
+    "it is not part of this build, which runs MSDA on AMD GPUs through its HIP kernels "
+    "(Backend.HIP) and on CPU tensors in torch operators (Backend.EAGER)"
 )
 
 

@@ -122,9 +122,9 @@ def resolve_msda_attn(attention_weights: Tensor, method: str | Method) -> tuple[
 
 def select_backend(context: MSDAContext) -> list[Backend]:
     """The policy for ``backend=None``: GPU tensors (device type ``"cuda"``, HIP on
-    ROCm) run the HIP kernels in every dtype, float64 included. The reference sends
-    CPU tensors to its eager backend, which this build does not ship, so they raise
-    ``NoBackendError`` saying so rather than falling back silently."""
+    ROCm) run the HIP kernels in every dtype, float64 included, and nothing else: a
+    GPU call that the kernels cannot take raises ``NoBackendError``. CPU tensors run
+    the eager backend, as in the reference (registry/msda.py:204-205)."""
     return [Backend.HIP] if context.device.type == "cuda" else [Backend.EAGER]
 
 
@@ -215,8 +215,8 @@ def _msda_call(  # noqa: PLR0913
     ValueError
         If the operands disagree in rank, size, dtype or device.
     NoBackendError
-        If no backend can run the call: CPU tensors, or a shape the kernels do not
-        cover; the message gives the reason.
+        If no backend can run the call (a GPU shape the kernels do not cover, or a
+        tensor on another device type); the message gives the reason.
     KernelUnavailableError
         If the HIP library is not built.
 
@@ -227,7 +227,8 @@ def _msda_call(  # noqa: PLR0913
     fp32 (fp64 for float64) by the single owner of each element and stored once;
     the backward uses no memory beyond the three gradient tensors. Valid levels
     that share positions of ``S`` sum their contributions into the shared
-    ``grad_value`` elements.
+    ``grad_value`` elements. CPU tensors run torch operators in float32 (float64
+    for float64 values), with the backward by autograd.
     """
     raise NotImplementedError
 

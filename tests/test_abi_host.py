@@ -188,12 +188,12 @@ def small_operands(device="cpu", dtype=torch.float32):
     return value, shapes, starts, loc, attn
 
 
-def test_cpu_tensors_raise_no_backend_error():
-    from deformops_amd.core.errors import NoBackendError  # noqa: PLC0415
+def test_cpu_tensors_run_the_eager_backend():
+    from deformops_amd.backends.eager.msda import forward  # noqa: PLC0415
     from deformops_amd.registry import msda  # noqa: PLC0415
 
-    with pytest.raises(NoBackendError):
-        msda(*small_operands())
+    ops = small_operands()
+    torch.testing.assert_close(msda(*ops), forward(*ops), rtol=0, atol=0)
 
 
 @pytest.mark.parametrize(

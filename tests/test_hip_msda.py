@@ -736,10 +736,12 @@ def test_backend_selection_and_aliases(device):
     torch.testing.assert_close(
         torch.ops.deformops.msda_softmax(*w.operands(softmax=True)), msda(*w.operands(softmax=True), softmax=True)
     )
-    with pytest.raises(NoBackendError):
-        msda(*ops, backend=Backend.TRITON)
     with pytest.raises(NoBackendError, match="not part of this build"):
-        msda(*(t.cpu() for t in ops))
+        msda(*ops, backend=Backend.TRITON)
+    # The CPU backend takes CPU tensors only: never GPU ones, even when asked.
+    with pytest.raises(NoBackendError, match="does not support"):
+        msda(*ops, backend=Backend.EAGER)
+    torch.testing.assert_close(msda(*(t.cpu() for t in ops)), auto.cpu(), rtol=1e-5, atol=1e-6)
 
 
 def test_unsupported_head_dim_raises_no_backend_error(device):

@@ -228,11 +228,14 @@ def test_run_msda_derives_level_starts_and_passes_chunk_step():
     assert backend.calls[-1]["method"] is Method.SOFTMAX
 
 
-@pytest.mark.parametrize("backend", [None, Backend.HIP])
-def test_run_msda_cpu_tensors_reach_the_registry(backend):
+def test_run_msda_cpu_tensors_reach_the_registry():
+    """CPU tensors run the eager backend by default; HIP declines them."""
     value, shapes, loc, attn = small_operands()
+    starts = torch.cat([shapes.new_zeros(1), (shapes[:, 0] * shapes[:, 1]).cumsum(0)[:-1]])
+    out = run_msda(value, shapes, None, loc, attn, chunk_step=64, backend=None)
+    torch.testing.assert_close(out, eager_msda(value, shapes, starts, loc, attn), rtol=1e-5, atol=1e-6)
     with pytest.raises((NoBackendError, RuntimeError)):
-        run_msda(value, shapes, None, loc, attn, chunk_step=64, backend=backend)
+        run_msda(value, shapes, None, loc, attn, chunk_step=64, backend=Backend.HIP)
 
 
 # the drop-in modules on the CPU (oracle backend)

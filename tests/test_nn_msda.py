@@ -20,7 +20,7 @@ import torch
 from deformops_amd.core.errors import NoBackendError
 from deformops_amd.core.runtime import Method
 from deformops_amd.nn import MultiScaleDeformAttn2d
-from deformops_amd.registry import MSDABackend
+from deformops_amd.registry import Backend, MSDABackend
 from oracle.eager import eager_msda
 
 F32, F64, BF16 = torch.float32, torch.float64, torch.bfloat16
@@ -195,11 +195,27 @@ def test_sampling_locations_points_and_boxes():
         m.sampling_locations(q, torch.rand(B, Q, L, 3, dtype=F64), shapes)
 
 
-def test_cpu_tensors_raise_no_backend_error():
-    m = MultiScaleDeformAttn2d(dim=16, num_heads=2, num_levels=1)
-    shapes, starts, n = pyramid([[4, 4]])
+def test_cpu_layer_runs_the_eager_backend():
+    """Without a backend the layer's CPU call runs Backend.EAGER; it matches the same
+    layer over the oracle adapter, output and gradients; asking for HIP raises."""
+    torch.manual_seed(0)
+    m = MultiScaleDeformAttn2d(dim=16, num_heads=2, num_levels=2, num_points=4).to(F64)
+    shapes, starts, n = pyramid([[4, 4], [2, 2]])
+    g = torch.Generator().manual_seed(1)
+    q, ref, x = (torch.randn(1, 3, 16, generator=g, dtype=F64), torch.rand(1, 3, 2, 2, generator=g, dtype=F64),
+                 torch.randn(1, n, 16, generator=g, dtype=F64))
+    oracle_layer = copy.deepcopy(m)
+    oracle_layer.backend = EagerOracleBackend()
+    out = m(q, ref, x, shapes, starts)
+    want = oracle_layer(q, ref, x, shapes, starts)
+    assert rel_err(out, want) <= 1e-12
+    out.sum().backward()
+    want.sum().backward()
+    for (name, p), p_ref in zip(m.named_parameters(), oracle_layer.parameters(), strict=True):
+        assert rel_err(p.grad, p_ref.grad) <= 1e-10, name
+    m.backend = Backend.HIP
     with pytest.raises(NoBackendError):
-        m(torch.randn(1, 3, 16), torch.rand(1, 3, 1, 2), torch.randn(1, n, 16), shapes, starts)
+        m(q, ref, x, shapes, starts)
 
 
 def test_cpu_layer_with_the_oracle_backend():
