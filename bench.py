@@ -15,7 +15,12 @@ steps, untimed, for another 0.3 s (fresh allocator blocks are slower at first). 
 bracketed by HIP events on that stream) by its algorithmic bytes against 8 TB/s;
 ``roofline.backward_call`` rates the backward call alone, and ``roofline.gather``
 rates the forward kernel's corner gathers against the random-row gather rate of
-L1 and L2 that the row-gather probe (libmsda_probe.so) measures in the same run.
+L1 and L2 that the row-gather probe (libmsda_probe.so) measures in the same run
+(``l2_peak_128b_rows``: the same probe with 128-byte rows, whole cache lines).
+``roofline.l2_requests`` rates the forward kernel by L2 requests per second, the
+quantity that bounds it: its request count per launch from the counter pass in
+profiles/msda_config4_bf16_l2_requests.md (when that pass ran on the kernel and
+probe sources being measured) over its live call time, against the probe's.
 ``roofline.traffic`` is the HBM bytes of one fwd+bwd from the rocprofv3 counter
 passes in profiles/msda_config4_bf16_hbm_traffic.md, reported only when those
 passes ran on the kernel source being measured. ``cpu_baseline`` times the torch
@@ -55,6 +60,9 @@ PEAK_HBM_GBS = 8000.0
 DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 KERNEL_SOURCE = REPO / "deformops_amd" / "csrc" / "msda.hip"
 TRAFFIC_PROFILE = REPO / "profiles" / "msda_config4_bf16_hbm_traffic.md"
+PROBE_SOURCE = REPO / "deformops_amd" / "csrc" / "gather_probe.hip"
+REQUEST_PROFILE = REPO / "profiles" / "msda_config4_bf16_l2_requests.md"
+PROBE_BYTES = 2048 * 256 * 128 * 8 * 16  # bytes one probe launch gathers (see row_gather_rates)
 SETTLE_S = 0.3  # untimed seconds of the measured work before each timing (see settle_clocks)
 
 
@@ -186,25 +194,26 @@ def time_calls(w, steps: int, warmup: int, softmax: bool, bwd_flags: int) -> dic
 
 def row_gather_rates(device: torch.device) -> dict[str, float]:
     """GB/s of random 64-byte row gathers (4 lanes x 16 bytes each) from a 16 KiB buffer
-    (L1-resident on every CU) and a 2 MiB one (L2-resident on every XCD), from the
-    probe kernel of libmsda_probe.so; mean of 5 launches of 2048 x 256 threads."""
+    (L1-resident on every CU) and a 2 MiB one (L2-resident on every XCD), and of
+    random 128-byte rows (8 lanes, one cache line each) from the 2 MiB buffer, from
+    the probe kernel of libmsda_probe.so; mean of 5 launches of 2048 x 256 threads."""
     import ctypes  # noqa: PLC0415
 
     path = REPO / "deformops_amd" / "lib" / "libmsda_probe.so"
     probe = ctypes.CDLL(str(path))
     probe.msda_probe_row_gather.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
-                                            ctypes.c_void_p, ctypes.c_void_p]
+                                            ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     probe.msda_probe_row_gather.restype = ctypes.c_int
     blocks, iters, threads = 2048, 128, 256
     sink = torch.empty(blocks * threads, dtype=torch.int32, device=device)
     stream = torch.cuda.current_stream()
     rates = {}
-    for name, nbytes in (("l1", 16 << 10), ("l2", 2 << 20)):
+    for name, nbytes, row_bytes in (("l1", 16 << 10, 64), ("l2", 2 << 20, 64), ("l2_128", 2 << 20, 128)):
         buf = torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device=device)
-        rows = nbytes // 64
+        rows = nbytes // row_bytes
 
         def launch() -> None:
-            rc = probe.msda_probe_row_gather(buf.data_ptr(), rows, blocks, iters, sink.data_ptr(),
+            rc = probe.msda_probe_row_gather(buf.data_ptr(), rows, row_bytes, blocks, iters, sink.data_ptr(),
                                              stream.cuda_stream)
             if rc != 0:
                 raise RuntimeError("row-gather probe launch failed")
@@ -219,7 +228,7 @@ def row_gather_rates(device: torch.device) -> dict[str, float]:
             e.record(stream)
             e.synchronize()
             times.append(s.elapsed_time(e))
-        gathered = blocks * (threads // 64) * 16 * iters * 8 * 64  # waves x groups x rows x bytes
+        gathered = blocks * threads * iters * 8 * 16  # lanes x loads x 16 bytes
         rates[name] = gathered / (statistics.mean(times) * 1e-3) / 1e9
     return rates
 
@@ -238,6 +247,23 @@ def profiled_traffic() -> tuple[int | None, str]:
     if sha.group(1) != current:
         return None, "the counter profile was taken on another kernel source"
     return int(total.group(1)), f"rocprofv3 FETCH_SIZE x2 + WRITE_SIZE passes, {TRAFFIC_PROFILE.relative_to(REPO)}"
+
+
+def profiled_l2_requests() -> tuple[dict[str, int] | None, str]:
+    """L2 requests per launch of the MSDA kernels and of the 2 MiB, 64-byte-row probe
+    at the default workload, from the counter pass in profiles/, when it ran on these
+    kernel and probe sources; else ``None`` and why."""
+    if not REQUEST_PROFILE.exists():
+        return None, "no request profile committed"
+    text = REQUEST_PROFILE.read_text()
+    shas = dict(re.findall(r"(kernel|probe)_source_sha256:\s*([0-9a-f]{64})", text))
+    counts = {name: int(n) for name, n in re.findall(r"l2_requests_per_launch (\S+):\s*(\d+)", text)}
+    if "kernel" not in shas or "probe" not in shas or "msda_forward_kernel" not in counts or "probe_l2" not in counts:
+        return None, "the request profile states no source hashes or counts"
+    for key, path in (("kernel", KERNEL_SOURCE), ("probe", PROBE_SOURCE)):
+        if shas[key] != hashlib.sha256(path.read_bytes()).hexdigest():
+            return None, f"the request profile was taken on another {key} source"
+    return counts, f"rocprofv3 TCC_HIT_sum + TCC_MISS_sum pass, {REQUEST_PROFILE.relative_to(REPO)}"
 
 
 def host_cpu() -> dict:
@@ -384,6 +410,16 @@ def main() -> int:
     default = args.config == 4 and args.dtype == "bf16" and loc_dtype == torch.bfloat16 and not softmax
     traffic, traffic_source = profiled_traffic() if default and args.grad_value == "owner" else (
         None, "profiled for the default workload only")
+    requests, request_source = profiled_l2_requests() if default else (None, "profiled for the default workload only")
+    l2_requests: dict = {"kernel": "msda_forward_kernel", "source": request_source}
+    if requests is not None:
+        # Requests per second: the forward's profiled count over its live call time, and
+        # the probe's profiled count over its live launch time (from its GB/s).
+        achieved = requests["msda_forward_kernel"] / (calls["forward"] * 1e-3) / 1e9
+        peak = requests["probe_l2"] / (PROBE_BYTES / (gather["l2"] * 1e9)) / 1e9
+        l2_requests.update({"requests_per_launch": requests["msda_forward_kernel"], "achieved": round(achieved, 1),
+                            "peak": round(peak, 1), "unit": "G requests/s", "frac": round(achieved / peak, 4),
+                            "peak_source": "the 2 MiB 64-byte-row probe of this run (one L2 request per row)"})
 
     levels = "/".join(f"{h}x{w_}" for h, w_ in cfg.levels)
     queries = f"Q=S={S}" if cfg.queries is None else f"Q={Q}, S={S}"
@@ -440,12 +476,14 @@ def main() -> int:
                 "achieved": round(corner_gbs, 1),
                 "l1_peak": round(gather["l1"], 1),
                 "l2_peak": round(gather["l2"], 1),
+                "l2_peak_128b_rows": round(gather["l2_128"], 1),
                 "unit": "GB/s",
                 "frac_of_l2": round(corner_gbs / gather["l2"], 4),
                 "frac_of_l1": round(corner_gbs / gather["l1"], 4),
                 "peak_source": "random 64-byte row gathers from a 2 MiB (L2) and 16 KiB (L1) buffer, "
-                               "libmsda_probe.so, this run",
+                               "and 128-byte rows from the 2 MiB buffer, libmsda_probe.so, this run",
             },
+            "l2_requests": l2_requests,
         },
     }
     if not args.no_cpu_baseline:

@@ -12,12 +12,14 @@
 extern "C" {
 #endif
 
-/* Random 64-byte row gathers: `blocks` workgroups of 256 threads on `stream` (a
- * hipStream_t), each wave fetching iters * 8 rows of `buffer` (rows * 64 bytes, rows
- * a power of two, device memory) with one 16-byte load per lane, 4 lanes a row.
- * `sink` (device memory) takes one uint32 per thread. Returns 0, or 1 for bad
- * arguments or a failed launch. */
-int msda_probe_row_gather(const void* buffer, int64_t rows, int blocks, int iters, void* sink,
+/* Random row gathers: `blocks` workgroups of 256 threads on `stream` (a
+ * hipStream_t). Each lane makes iters * 8 loads of 16 bytes; row_bytes / 16 lanes
+ * (4 for 64-byte rows, 8 for 128-byte rows) fetch one pseudo-random row of `buffer`
+ * (rows * row_bytes bytes, rows a power of two, device memory) per load, so a wave
+ * load gathers 1 KiB either way. `sink` (device memory) takes one uint32 per
+ * thread. Returns 0, or 1 for bad arguments (row_bytes other than 64 or 128) or a
+ * failed launch. */
+int msda_probe_row_gather(const void* buffer, int64_t rows, int row_bytes, int blocks, int iters, void* sink,
                           void* stream);
 
 #ifdef __cplusplus

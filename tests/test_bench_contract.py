@@ -66,3 +66,13 @@ def test_cpu_baseline_sample_is_bounded(config, monkeypatch):
     queries = 300 if config == 1 else 21504
     assert samples == [(1, min(queries, 21504))]
     assert f"x{cfg.batch * queries / min(queries, 21504):g}" in line["sample"]
+
+
+def test_committed_request_profile_parses_for_the_committed_sources():
+    """profiles/msda_config4_bf16_l2_requests.md carries the forward's and the probe's
+    L2 request counts, taken on the kernel and probe sources in the tree."""
+    import bench  # noqa: PLC0415
+
+    counts, source = bench.profiled_l2_requests()
+    assert counts is not None, source
+    assert counts["msda_forward_kernel"] > 0 and counts["probe_l2"] > counts["probe_l2_128"] > 0
