@@ -88,3 +88,27 @@ def test_largest_image_addressable_with_32_bit_offsets(device, dtype, shape):
         assert rel_err(ga[:, qs], rga.reshape(ga[:, qs].shape)) <= BWD_TOL[dtype]
     # No sample reaches the rows between the bands.
     assert gv[:, BAND:Hh - BAND].abs().amax().item() == 0.0
+
+
+# Many samples per (query, head): the staged records of one unit grow with L * P, and
+# where a wave's units would not fit its LDS budget a unit takes more lanes than its
+# channels need (msda_launch_geometry; tests/test_abi_host.py). L * P = 128 gives a
+# bf16 unit of D = 32 8 lanes for the 4 its channels need; L * P = 512 with D = 8
+# takes 32 lanes for 2.
+MANY = [
+    pytest.param(((12, 12), (6, 6), (3, 3), (2, 2)), 32, 32, torch.bfloat16, id="lp128-bf16"),
+    pytest.param(((12, 12), (6, 6), (3, 3), (2, 2)), 32, 32, torch.float32, id="lp128-f32"),
+    pytest.param(((16, 16), (4, 4)), 256, 8, torch.float32, id="lp512-d8-f32"),
+]
+
+
+@pytest.mark.parametrize(("levels", "P", "D", "dtype"), MANY)
+def test_many_samples_per_unit(device, levels, P, D, dtype):
+    from tests.test_hip_msda import check_against_oracle  # noqa: PLC0415
+    from tests.workloads import make_workload  # noqa: PLC0415
+
+    w = make_workload(0, levels=levels, batch=2, queries=37, heads=3, channels=D, points=P,
+                      locations="uniform", seed=P).to(device, dtype)
+    for softmax in (False, True):
+        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                             label=f"L*P={len(levels) * P} D={D}")
