@@ -15,6 +15,8 @@ import math
 
 import pytest
 import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
 
 import oracle
 from deformops_amd.core.errors import NoBackendError
@@ -175,3 +177,36 @@ def test_explicit_backends_on_cpu_tensors():
         msda(*ops, backend=Backend.HIP)
     with pytest.raises(NoBackendError, match="not part of this build"):
         msda(*ops, backend=Backend.TRITON)
+
+
+# Random shapes, as the GPU sweep draws them (tests/test_hip_msda_hypothesis.py),
+# smaller so that the CPU suite stays quick; derandomized, so every run replays the
+# same cases.
+
+
+@st.composite
+def cases(draw):
+    L = draw(st.integers(1, 4))
+    return {
+        "levels": tuple((draw(st.integers(1, 24)), draw(st.integers(1, 24))) for _ in range(L)),
+        "batch": draw(st.integers(1, 2)),
+        "queries": draw(st.integers(1, 40)),
+        "heads": draw(st.sampled_from([1, 2, 3, 8])),
+        "channels": draw(st.sampled_from([1, 7, 8, 32])),
+        "points": draw(st.integers(1, 6)),
+        "seed": draw(st.integers(0, 2**31 - 1)),
+        "dtype": draw(st.sampled_from([F64, F32, BF16, F16])),
+        "softmax": draw(st.booleans()),
+        "locations": draw(st.sampled_from(["uniform", "reference"])),
+    }
+
+
+@given(case=cases())
+@settings(max_examples=60, deadline=None, derandomize=True, database=None,
+          suppress_health_check=[HealthCheck.too_slow, HealthCheck.data_too_large])
+def test_random_shapes_match_oracle(case):
+    w = make_workload(0, levels=case["levels"], batch=case["batch"], queries=case["queries"], heads=case["heads"],
+                      channels=case["channels"], points=case["points"], seed=case["seed"],
+                      locations=case["locations"]).to("cpu", case["dtype"])
+    check(*w.operands(softmax=case["softmax"]), w.grad_output, softmax=case["softmax"], dtype=case["dtype"],
+          label=str(case))
