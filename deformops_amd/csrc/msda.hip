@@ -271,6 +271,29 @@ template <typename A> __device__ inline A unit_max(A v, int lh) {
   return v;
 }
 
+// The sums over a unit's lh lanes (4 or 8) of eight values per lane, reduce-scattered:
+// each halving step swaps the half of its values a lane does not keep with its
+// partner, so the steps move 4, 2 (and 1) values instead of 8 each. Lane t of the
+// unit ends with value t (lh = 8) or values 2 t and 2 t + 1 (lh = 4) in v[0] (v[1]).
+template <int CTRL, int N> __device__ inline void halve(float (&v)[8], bool hi) {
+#pragma unroll
+  for (int j = 0; j < N / 2; ++j) {
+    const float send = hi ? v[j] : v[N / 2 + j];
+    const float keep = hi ? v[N / 2 + j] : v[j];
+    v[j] = keep + quad_perm<CTRL>(send);
+  }
+}
+__device__ inline void unit_reduce_scatter8(float (&v)[8], int lh, int t) {
+  if (lh == 8) {
+    halve<kRowHalfMirror, 8>(v, (t & 4) != 0);  // lane i pairs with 7 - i
+    halve<kQuadXor2, 4>(v, (t & 2) != 0);
+    halve<kQuadXor1, 2>(v, (t & 1) != 0);
+  } else {
+    halve<kQuadXor2, 8>(v, (t & 2) != 0);
+    halve<kQuadXor1, 4>(v, (t & 1) != 0);
+  }
+}
+
 __device__ inline float exp_acc(float x) { return __expf(x); }
 __device__ inline double exp_acc(double x) { return exp(x); }
 
@@ -2662,10 +2685,12 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
 constexpr int kSampleBatch = 2;
 
 // G_c = <grad_out, value at corner c> for the staged samples s .. s + N - 1 of the
-// lane's unit, summed over the unit's lanes; the lane that staged a sample keeps its
-// G_c in the sample's slot. The corner loads of all N samples go out before the
-// first dot product (the cross-lane sums keep the compiler from unrolling a loop
-// over samples).
+// lane's unit, summed over the unit's lanes, into the samples' slots. The corner
+// loads of all N samples go out before the first dot product (the cross-lane sums
+// keep the compiler from unrolling a loop over samples). For two samples in units of
+// 4 or 8 float lanes the eight sums are reduce-scattered (unit_reduce_scatter8) and
+// each lane stores the ones it ends with; otherwise every lane forms all the sums and
+// the lane that staged a sample stores its four.
 template <typename T, int CV, int N>
 __device__ inline void corner_dots(const LaneMap& m, Staged<typename Elem<T>::acc>* wst, int s, bool lane_ok,
                                    const char* img, uint32_t lane_bytes, const typename Chan<T, CV>::R& g) {
@@ -2689,6 +2714,22 @@ __device__ inline void corner_dots(const LaneMap& m, Staged<typename Elem<T>::ac
     for (int n = 0; n < N; ++n)
 #pragma unroll
       for (int c = 0; c < 4; ++c) G[n][c] = Chan<T, CV>::dot(g, v[n][c], G[n][c]);
+  }
+  if constexpr (N == 2 && __is_same(A, float)) {
+    if (m.lh == 4 || m.lh == 8) {
+      float v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = G[i >> 2][i & 3];
+      unit_reduce_scatter8(v, m.lh, m.t);
+      if (m.unit_ok) {
+        // Lane t holds sum t (lh = 8) or sums 2 t, 2 t + 1 (lh = 4); sum i is sample
+        // s + i / 4, corner i % 4.
+        const int i0 = m.lh == 8 ? m.t : 2 * m.t;
+        wst[(s + (i0 >> 2)) * m.uw_count + m.uw].w[i0 & 3] = v[0];
+        if (m.lh == 4) wst[(s + (i0 >> 2)) * m.uw_count + m.uw].w[(i0 & 3) + 1] = v[1];
+      }
+      return;
+    }
   }
 #pragma unroll
   for (int n = 0; n < N; ++n)
@@ -2768,6 +2809,7 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
   for (; s + kSampleBatch <= LP; s += kSampleBatch)
     corner_dots<T, CV, kSampleBatch>(m, wst, s, lane_ok, img, lane_bytes, g);
   for (; s < LP; ++s) corner_dots<T, CV, 1>(m, wst, s, lane_ok, img, lane_bytes, g);
+  wave_lds_order();  // other lanes of the unit stored some of a sample's sums
 
   // Per-sample location and weight gradients by the lane that staged the sample.
   const TL* loc = reinterpret_cast<const TL*>(raw.loc);
