@@ -60,7 +60,7 @@ PEAK_HBM_GBS = 8000.0
 DTYPES = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
 KERNEL_SOURCE = REPO / "deformops_amd" / "csrc" / "msda.hip"
 TRAFFIC_PROFILE = REPO / "profiles" / "msda_config4_bf16_hbm_traffic.md"
-PROBE_SOURCE = REPO / "deformops_amd" / "csrc" / "gather_probe.hip"
+PROBE_SOURCE = REPO / "bench_probe" / "gather_probe.hip"
 REQUEST_PROFILE = REPO / "profiles" / "msda_config4_bf16_l2_requests.md"
 PROBE_BYTES = 2048 * 256 * 128 * 8 * 16  # bytes one probe launch gathers (see row_gather_rates)
 SETTLE_S = 0.3  # untimed seconds of the measured work before each timing (see settle_clocks)
@@ -196,10 +196,10 @@ def row_gather_rates(device: torch.device) -> dict[str, float]:
     """GB/s of random 64-byte row gathers (4 lanes x 16 bytes each) from a 16 KiB buffer
     (L1-resident on every CU) and a 2 MiB one (L2-resident on every XCD), and of
     random 128-byte rows (8 lanes, one cache line each) from the 2 MiB buffer, from
-    the probe kernel of libmsda_probe.so; mean of 5 launches of 2048 x 256 threads."""
+    the probe kernel of bench_probe/libmsda_probe.so; mean of 5 launches of 2048 x 256 threads."""
     import ctypes  # noqa: PLC0415
 
-    path = REPO / "deformops_amd" / "lib" / "libmsda_probe.so"
+    path = REPO / "bench_probe" / "libmsda_probe.so"
     probe = ctypes.CDLL(str(path))
     probe.msda_probe_row_gather.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]

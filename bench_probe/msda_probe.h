@@ -1,7 +1,7 @@
 /*
- * libmsda_probe.so: measurement probes for the MSDA library, not part of its drop-in
- * boundary (no counterpart in the reference). bench.py uses them to state the
- * ceilings the MSDA kernels are rated against.
+ * bench_probe/libmsda_probe.so: measurement probes for bench.py, not part of the
+ * MSDA library or its drop-in boundary (no counterpart in the reference). bench.py
+ * uses them to state the ceilings the MSDA kernels are rated against.
  */
 #ifndef MSDA_PROBE_H_
 #define MSDA_PROBE_H_

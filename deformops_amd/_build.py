@@ -1,9 +1,8 @@
-"""Ahead-of-time build of the HIP libraries for gfx950.
+"""Ahead-of-time build of the HIP library for gfx950.
 
-libdeformops_amd.so is the MSDA library (the C ABI of include/deformops_amd.h);
-libmsda_probe.so holds the measurement probes bench.py rates the kernels against
-(include/msda_probe.h). Both are built in-tree (``deformops_amd/lib/``) with hipcc
-and loaded with ctypes; nothing is compiled at import or call time.
+libdeformops_amd.so is the MSDA library (the C ABI of include/deformops_amd.h),
+built in-tree (``deformops_amd/lib/``) with hipcc and loaded with ctypes; nothing is
+compiled at import or call time.
 
     python -m deformops_amd._build
 """
@@ -17,15 +16,13 @@ import sys
 import tempfile
 from pathlib import Path
 
-__all__ = ["ARCH", "HIPCC_FLAGS", "LIBRARY", "PROBE_LIBRARY", "SOURCES", "build"]
+__all__ = ["ARCH", "HIPCC_FLAGS", "LIBRARY", "SOURCES", "build", "compile_library"]
 
 PACKAGE_DIR = Path(__file__).resolve().parent
 REPO_DIR = PACKAGE_DIR.parent
 SOURCES = [PACKAGE_DIR / "csrc" / "msda.hip"]
 INCLUDE_DIR = REPO_DIR / "include"
 LIBRARY = PACKAGE_DIR / "lib" / "libdeformops_amd.so"
-PROBE_SOURCES = [PACKAGE_DIR / "csrc" / "gather_probe.hip"]
-PROBE_LIBRARY = PACKAGE_DIR / "lib" / "libmsda_probe.so"
 ARCH = os.environ.get("DEFORMOPS_AMD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [
@@ -52,18 +49,17 @@ def _hipcc() -> str:
 
 
 def build(*, verbose: bool = False) -> Path:
-    """Compile both libraries, atomically replacing each; return the MSDA library's path.
+    """Compile the MSDA library, atomically replacing it; return its path.
 
     Raises
     ------
     subprocess.CalledProcessError
         If hipcc fails; the compiler output is in the exception.
     """
-    _compile(PROBE_SOURCES, PROBE_LIBRARY, verbose=verbose)
-    return _compile(SOURCES, LIBRARY, verbose=verbose)
+    return compile_library(SOURCES, LIBRARY, verbose=verbose)
 
 
-def _compile(sources: list[Path], target: Path, *, verbose: bool) -> Path:
+def compile_library(sources: list[Path], target: Path, *, verbose: bool) -> Path:
     target.parent.mkdir(parents=True, exist_ok=True)
     fd, tmp = tempfile.mkstemp(prefix=target.name + ".", suffix=".tmp", dir=target.parent)
     os.close(fd)

@@ -1,1 +1,1 @@
-"""Backend adapters. This build has one: ``hip``, the gfx950 kernels."""
+"""Backend adapters: ``hip`` (the gfx950 kernels, GPU tensors) and ``eager`` (torch operators, CPU tensors)."""

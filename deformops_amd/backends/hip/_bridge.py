@@ -212,6 +212,7 @@ def _define(prefix: str, *, softmax: bool) -> tuple[Any, Any]:
         ctx.save_for_backward(value, spatial_shapes, level_start_index, loc, attn)
         ctx.options = tuple(options)
 
+    @torch.autograd.function.once_differentiable
     def backward(ctx, grad_output):  # noqa: ANN001, ANN202
         value, spatial_shapes, level_start_index, loc, attn = ctx.saved_tensors
         grad_value, grad_loc, grad_attn = bwd_op(
@@ -246,7 +247,10 @@ class _EagerMSDA(torch.autograd.Function):
         return _launch_forward(value, spatial_shapes, level_start_index, loc, attn, softmax=softmax)
 
     @staticmethod
+    @torch.autograd.function.once_differentiable
     def backward(ctx, grad_output):  # noqa: ANN001, ANN205
+        # The kernels' gradients carry no graph: a second derivative raises, as the
+        # reference's CUDA bridge does (cuda/_msda_bridge.py:232).
         value, spatial_shapes, level_start_index, loc, attn = ctx.saved_tensors
         grad_value, grad_loc, grad_attn = _launch_backward(
             value, spatial_shapes, level_start_index, loc, attn, grad_output, softmax=ctx.softmax

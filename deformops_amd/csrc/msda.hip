@@ -366,6 +366,12 @@ struct Problem {
   int num_blocks;
   int loc_piece, attn_piece;  // bytes per lane access copying a wave's records to LDS
   int atomic_gv;              // backward: grad_sample scatters grad_value with atomics
+  // Backward on the matrix-core owners: levels that share positions of S are sorted
+  // too (each level's tiles are its own buckets); the count pass zeroes grad_value
+  // (when zero_gv) and the owners add their fp32 sums with atomics.
+  int sort_overlap;
+  int zero_gv;  // grad_value starts at zero (not accumulated into)
+  int es;       // bytes of one value element
 };
 
 // One pyramid level as the kernels use it. A level whose table entry does not fit
@@ -635,10 +641,12 @@ __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const L
     Staged<A> st;
 #pragma unroll
     for (int c = 0; c < 4; ++c) st.off[c] = g.off[c];
-    st.w[0] = g.w00 * a;
-    st.w[1] = g.w01 * a;
-    st.w[2] = g.w10 * a;
-    st.w[3] = g.w11 * a;
+    // A corner outside the level weighs exactly zero, whatever the attention weight
+    // (0 * inf would be NaN): the reference skips such corners.
+    st.w[0] = g.m00 ? g.w00 * a : A(0);
+    st.w[1] = g.m01 ? g.w01 * a : A(0);
+    st.w[2] = g.m10 ? g.w10 * a : A(0);
+    st.w[3] = g.m11 ? g.w11 * a : A(0);
     wst[s * m.uw_count + m.uw] = st;
   }
 }
@@ -922,9 +930,10 @@ __device__ inline typename Elem<T>::acc unit_weight(const T* unit_attn, int LP, 
 
 // Shared set-up of the bucketing kernels and the owners: the level table and the
 // tiles in LDS. Returns the tile count of one (b, h), or -1 when there are too many
-// tiles or when valid levels overlap (`overlap` then says so): the sort and the
-// owners then stand aside, and msda_grad_sample_kernel scatters grad_value with
-// atomics.
+// tiles. When valid levels overlap (`overlap` then says so), the matrix-core owners
+// take them too (sort_overlap) and add into a zeroed grad_value; otherwise -1: the
+// sort and the owners stand aside, and msda_grad_sample_kernel scatters grad_value
+// with atomics.
 __device__ inline int64_t load_tiles(const Problem& p, const BwdGeom& bg, Level* levels,
                                      LevelTiles* lt, int64_t* total_out, bool* overlap = nullptr) {
   if (threadIdx.x == 0) *overlap_flag() = 0;
@@ -935,7 +944,7 @@ __device__ inline int64_t load_tiles(const Problem& p, const BwdGeom& bg, Level*
   __syncthreads();
   const bool any = *overlap_flag() != 0;
   if (overlap) *overlap = any;
-  return any ? -1 : *total_out;
+  return any && !p.sort_overlap ? -1 : *total_out;
 }
 
 // The per-workgroup count rows of the chunked bucket sort, nkeys ints for each
@@ -989,6 +998,42 @@ __device__ inline bool softmax_stats_fit(const Problem& p, const BwdGeom& bg, in
   return need <= bh * bg.keys_alloc && at % alignof(SoftStat<A>) == 0;
 }
 
+// The gradients of one sample from its corner dots G_c = <grad_out, value at corner
+// c> (ignored for corners outside the level): with respect to its weight,
+// sum_c bilinear_c G_c; with respect to its normalized location, the attention
+// weight a times the derivatives of the bilinear weights (pixel units, scaled by the
+// level's width and height). A sample outside the level has no corner: its location
+// gradient is zero whatever its weight (the reference skips it). Without
+// contraction, as the eager reference's separate tensor operations round.
+template <typename A>
+__device__ inline void sample_grads(const Geom<A>& ge, A a, const Level& lv, A g00, A g01, A g10, A g11, A* gx,
+                                    A* gy, A* gpv) {
+#pragma clang fp contract(off)
+  const A G00 = ge.m00 ? g00 : A(0);
+  const A G01 = ge.m01 ? g01 : A(0);
+  const A G10 = ge.m10 ? g10 : A(0);
+  const A G11 = ge.m11 ? g11 : A(0);
+  const A one(1);
+  *gpv = ge.w00 * G00 + ge.w01 * G01 + ge.w10 * G10 + ge.w11 * G11;
+  *gx = ge.in ? a * A(lv.w) * ((one - ge.dy) * (G01 - G00) + ge.dy * (G11 - G10)) : A(0);
+  *gy = ge.in ? a * A(lv.h) * ((one - ge.dx) * (G10 - G00) + ge.dx * (G11 - G01)) : A(0);
+}
+
+// Overlapping levels on the matrix-core owners: the count pass zeroes grad_value
+// (its workgroups, grid-stride, 16 bytes a thread) before the owners add into it; the
+// keys then stay out of grad_value and the place pass recomputes them.
+__device__ inline void zero_grad_value(const Problem& p) {
+  const int64_t bytes = int64_t(p.B) * p.S * p.H * p.D * p.es;
+  const int64_t stride = int64_t(gridDim.x) * blockDim.x;
+  const int64_t first = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (bytes % 16 == 0 && reinterpret_cast<uintptr_t>(p.grad_value) % 16 == 0) {
+    const u32x4_v zero = {0u, 0u, 0u, 0u};
+    for (int64_t i = first; i < bytes / 16; i += stride) reinterpret_cast<u32x4_v*>(p.grad_value)[i] = zero;
+  } else {
+    for (int64_t i = first; i < bytes / 2; i += stride) reinterpret_cast<uint16_t*>(p.grad_value)[i] = 0;
+  }
+}
+
 // Counting (PLACE = false) or placing (PLACE = true) pass of the bucket sort.
 // Workgroup: kBucketThreads * kBucketSamples consecutive samples (q, l, p) of one
 // (b, h). `buckets` holds one counter per bucket and (b, h): counts after the count
@@ -1009,9 +1054,11 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket_kernel(const Probl
   const size_t head = ((sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) + 15) & ~size_t(15);
   int64_t* total = reinterpret_cast<int64_t*>(smem + head);
   int* hist = reinterpret_cast<int*>(smem + head + 16);
-  const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
+  bool overlap = false;
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total, &overlap);
   const int64_t nkeys = 4 * ntiles;
   if (ntiles < 0 || nkeys > bg.keys_alloc) return;  // no bucketing: the owners scan
+  if (!PLACE && overlap && p.zero_gv) zero_grad_value(p);
   const bool in_lds = nkeys <= bg.keys_lds;
   // Groups (b, chunk), the heads of a group on one XCD: they share the cache lines of
   // their queries' locations.
@@ -1149,9 +1196,14 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
   const size_t head = ((sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) + 15) & ~size_t(15);
   int64_t* total = reinterpret_cast<int64_t*>(smem + head);
   int* hist = reinterpret_cast<int*>(smem + head + 16);
-  const int64_t ntiles = load_tiles(p, bg, levels, lt, total);
+  bool overlap = false;
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total, &overlap);
   const int64_t nkeys = 4 * ntiles;
   if (ntiles < 0 || nkeys > bg.keys_alloc) return;  // no bucketing: the owners scan
+  // Overlapping levels: grad_value is zeroed for the owners' atomic adds, so the place
+  // pass recomputes the keys instead of reading them back.
+  const bool keep_keys = !overlap;
+  if (!PLACE && overlap && p.zero_gv) zero_grad_value(p);
   const bool in_lds = nkeys <= bg.keys_lds;
   int group, h;
   if (!xcd_group_block(p.H, p.B * chunks_per_bh, &group, &h)) return;
@@ -1196,7 +1248,7 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
     for (int i = 0; i < 4; ++i) k[i] = sample_key<A>(xy[2 * i], xy[2 * i + 1], lv, tl);
   };
   auto save = [&](int64_t g, const int (&k)[4]) __attribute__((always_inline)) {
-    if (g >= ngroups) return;
+    if (g >= ngroups || !keep_keys) return;
     Word w;
     if constexpr (KB == 2) {
       w[0] = (uint32_t(k[0]) & 0xffffu) | (uint32_t(k[1]) << 16);
@@ -1208,6 +1260,10 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
     keys[g] = w;
   };
   auto restore = [&](int64_t g, int (&k)[4]) __attribute__((always_inline)) {
+    if (!keep_keys) {
+      keys_of(g, k);
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) k[i] = -1;
     if (g >= ngroups) return;
@@ -2334,8 +2390,20 @@ __device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, con
 template <typename T, int NB>
 __device__ inline void mfma_store_subtile(const Problem& p, const Level& lv, const MfmaTile& t, int b, int h,
                                           int st, const f32x4_v (&c)[NB], int g16, int i16, int accumulate,
-                                          T* gv) {
+                                          T* gv, bool add = false) {
   constexpr int D = 16 * NB;
+  // add: overlapping levels. Tiles of two levels own the shared positions, so each
+  // adds its fp32 sums with one atomic per element (float) or per channel pair
+  // (16-bit: the even lane adds its pair, the odd lane's value taken with a DPP move
+  // before any lane branches): one rounding for the sum and one for the add per
+  // level, where a 16-bit atomic scatter rounds once per contribution.
+  f32x4_v pair[NB];
+  if constexpr (sizeof(T) == 2)
+    if (add)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pair[nb][r] = quad_perm<kQuadXor1>(c[nb][r]);
   const int y = t.r0 + 4 * (st >> 1) + g16;
   if (y >= t.r1) return;
 #pragma unroll
@@ -2346,6 +2414,22 @@ __device__ inline void mfma_store_subtile(const Problem& p, const Level& lv, con
       T* dst = gv + (pos * p.H + h) * D + i16;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
+        if (add) {
+          if constexpr (std::is_same_v<T, float>) {
+            unsafeAtomicAdd(dst + 16 * nb, c[nb][r]);
+          } else if constexpr (std::is_same_v<T, bf16_t>) {
+            if ((i16 & 1) == 0) {
+              const bf16x2_v v2 = {static_cast<__bf16>(c[nb][r]), static_cast<__bf16>(pair[nb][r])};
+              __builtin_amdgcn_global_atomic_fadd_v2bf16(reinterpret_cast<bf16x2_v*>(dst + 16 * nb), v2);
+            }
+          } else {
+            if ((i16 & 1) == 0) {
+              const f16x2_v v2 = {static_cast<_Float16>(c[nb][r]), static_cast<_Float16>(pair[nb][r])};
+              __builtin_amdgcn_global_atomic_fadd_v2f16(reinterpret_cast<f16x2_v*>(dst + 16 * nb), v2);
+            }
+          }
+          continue;
+        }
         float v = c[nb][r];
         if (accumulate) v += load_acc(dst + 16 * nb);
         store_elem(dst + 16 * nb, v);
@@ -2439,10 +2523,12 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
 
   bool overlap;
   const int64_t ntiles = load_tiles(p, bg, levels, lt, total, &overlap);
-  if (!accumulate) {
+  // Overlapping levels on the owners: the count pass zeroed grad_value, and the owners add.
+  const bool add = p.sort_overlap && overlap;
+  if (!accumulate && !add) {
     // grad_value at positions no valid level covers is zero (the tiles own all the
-    // others, so this never meets their stores); when levels overlap, every
-    // position starts at zero for the atomic scatter.
+    // others, so this never meets their stores); when levels overlap and the owners
+    // stand aside, every position starts at zero for the atomic scatter.
     const int64_t n = int64_t(p.B) * p.S;
     for (int64_t idx = int64_t(blockIdx.x) * blockDim.x + tid; idx < n; idx += int64_t(gridDim.x) * blockDim.x) {
       const int pos = int(idx % p.S);
@@ -2651,7 +2737,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
         // (r0 + 4 (st / 2) + g, c0 + 4 (st % 2) + r), channel 16 nb + i.
 #pragma unroll
         for (int st = 0; st < 4; ++st)
-          mfma_store_subtile<T, NB>(p, lv, t, b, h, st, acc[st], g16, i16, accumulate, gv);
+          mfma_store_subtile<T, NB>(p, lv, t, b, h, st, acc[st], g16, i16, accumulate, gv, add);
         continue;
       }
       // Partial sums meet in LDS (each wave's own region, which only it used so
@@ -2673,7 +2759,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
           sum[nb] += __builtin_bit_cast(
               f32x4_v, reinterpret_cast<const u32x4_v*>(region0 + size_t(w) * kWaveBytes)[(wave * NB + nb) * kWave + lane]);
       }
-      mfma_store_subtile<T, NB>(p, lv, t, b, h, wave, sum, g16, i16, accumulate, gv);
+      mfma_store_subtile<T, NB>(p, lv, t, b, h, wave, sum, g16, i16, accumulate, gv, add);
       __syncthreads();  // the partial sums are read before the next tile reuses the LDS
       mfma_zero_tiles(wt, lane);
     }
@@ -2779,9 +2865,9 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
   A smax, sinv;
   stage_samples<T, TL, SOFTMAX>(p, m, levels, raw, wst, smax, sinv);
   __syncthreads();
-  // grad_value by atomics: asked for, or levels overlap (the sort and the owners then
-  // only zeroed grad_value).
-  const bool scatter = *overlap_flag() != 0 || p.atomic_gv;
+  // grad_value by atomics: asked for, or levels overlap where the owners stand aside
+  // (the sort and the owners then only zeroed grad_value).
+  const bool scatter = (*overlap_flag() != 0 && !p.sort_overlap) || p.atomic_gv;
 
   // Gather the corners and form G_c; the lane that staged sample s keeps its G_c
   // in the sample's slot.
@@ -2827,14 +2913,8 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
       A a = load_acc(attn + s);
       if constexpr (SOFTMAX) a = exp_acc(a - smax) * sinv;
       Staged<A>* slot = wst + s * m.uw_count + m.uw;
-      const A G00 = ge.m00 ? slot->w[0] : A(0);
-      const A G01 = ge.m01 ? slot->w[1] : A(0);
-      const A G10 = ge.m10 ? slot->w[2] : A(0);
-      const A G11 = ge.m11 ? slot->w[3] : A(0);
-      const A one(1);
-      const A gpv = ge.w00 * G00 + ge.w01 * G01 + ge.w10 * G10 + ge.w11 * G11;
-      const A gx = a * A(lv.w) * ((one - ge.dy) * (G01 - G00) + ge.dy * (G11 - G10));
-      const A gy = a * A(lv.h) * ((one - ge.dx) * (G10 - G00) + ge.dx * (G11 - G01));
+      A gx, gy, gpv;
+      sample_grads<A>(ge, a, lv, slot->w[0], slot->w[1], slot->w[2], slot->w[3], &gx, &gy, &gpv);
       store_loc_pair(gloc + 2 * s, gx, gy);
       if constexpr (SOFTMAX) {
         dot += a * gpv;
@@ -3552,6 +3632,11 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   p.grad_loc = static_cast<char*>(grad_sampling_locations);
   p.grad_attn = static_cast<char*>(grad_attention_weights);
   p.atomic_gv = atomic_gv ? 1 : 0;
+  // The matrix-core owners take overlapping levels when nothing falls back to the
+  // VALU owner kernel (which stores, and stands aside on overlap).
+  p.sort_overlap = plan.bucket && plan.mfma && !plan.mfma_fallback && !atomic_gv ? 1 : 0;
+  p.zero_gv = accumulate ? 0 : 1;
+  p.es = es;
   if (atomic_gv && !accumulate) {  // the atomic scatter adds into zeros
     rc = zero_fill(grad_value, value_bytes, st, "msda_backward");
     if (rc != MSDA_OK) return rc;

@@ -248,10 +248,12 @@ def test_public_ops_carry_the_reference_schema():
 
 
 def test_probe_library_exports_its_header():
-    """libmsda_probe.so (bench.py's row-gather probe) exports what include/msda_probe.h declares."""
-    header = HEADER.parent / "msda_probe.h"
-    declared = re.findall(r"^int\s+(msda_\w+)\(", header.read_text(), flags=re.M)
+    """bench_probe/libmsda_probe.so (bench.py's row-gather probe, outside the product
+    package) exports what bench_probe/msda_probe.h declares."""
+    probe_dir = Path(__file__).resolve().parents[1] / "bench_probe"
+    declared = re.findall(r"^int\s+(msda_\w+)\(", (probe_dir / "msda_probe.h").read_text(), flags=re.M)
     assert declared == ["msda_probe_row_gather"]
-    probe = ctypes.CDLL(str(Path(_lib.library_path()).parent / "libmsda_probe.so"))
+    probe = ctypes.CDLL(str(probe_dir / "libmsda_probe.so"))
     for name in declared:
         assert hasattr(probe, name)
+

