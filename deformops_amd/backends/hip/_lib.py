@@ -26,6 +26,7 @@ __all__ = [
     "FLAG_SOFTMAX",
     "PATH_ATOMIC_SORT",
     "PATH_NO_MFMA",
+    "PATH_TILE8",
     "INDEX_CODES",
     "EXPORTED_SYMBOLS",
     "Library",
@@ -53,6 +54,7 @@ FLAG_GRAD_VALUE_ATOMIC = 4
 #: enum msda_path_bits.
 PATH_NO_MFMA = 1
 PATH_ATOMIC_SORT = 2
+PATH_TILE8 = 4
 
 #: Every function the header declares.
 EXPORTED_SYMBOLS = (

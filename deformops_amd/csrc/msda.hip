@@ -750,8 +750,14 @@ constexpr int kOwnerItems = 4;      // (position, channel group) items per threa
 constexpr int kOwnerChunks = 4;     // grad_out pieces one thread stages per batch
 constexpr int kBucketThreads = 256;
 constexpr int kBucketSamples = 32;  // samples per thread in the bucketing kernels
-constexpr int kBucketBatch = 8;     // of which loaded together
+constexpr int kBucketSamplesSmall = 4;  // the same for small calls (a short latency chain per thread)
+constexpr int kBucketBatch = 8;     // of which loaded together (at most)
 constexpr int kTargetRecords = 8192;
+// A level takes 4 x 4 tiles below this many 8 x 8 tasks (B H tiles; about 1.5 per CU:
+// more overlap with other levels' work, as at config 4's 512) and from this many
+// K-blocks per 8 x 8 task.
+constexpr int kSmallTileTasks = 384;
+constexpr int kSmallTileKBlocks = 24;
 constexpr int kBucketLdsKeys = 8192;  // LDS bucket counters of the bucketing kernels (32 KB)
 constexpr int kMaxOrderedLevels = 64;
 // Scratch ints after the bucket rows for the matrix-core kernel's kXcds work-queue
@@ -795,7 +801,8 @@ struct BwdGeom {
   int64_t region;   // entries per (b, h): Q * L * P
   FastDiv div_lp;   // by L * P
   FastDiv div_p;    // by P
-  int sub_log2;     // > 0: every tile is 2^sub_log2 square (the matrix-core grad_value)
+  int sub_log2;     // > 0: tiles are 2^sub_log2 square (the matrix-core grad_value)
+  int small_tiles;  // matrix-core grad_value: levels with few heavy tiles take 4 x 4 tiles
   int group4;       // samples go in groups of 4 of one query and level (L P and P multiples of 4)
   FastDiv div_gpq;  // by L * P / 4, groups per query
   FastDiv div_gpl;  // by P / 4, groups per level
@@ -837,7 +844,17 @@ __device__ inline int64_t plan_tiles(const Problem& p, const BwdGeom& bg, const 
     const Level lv = levels[l];
     LevelTiles t{0, 0, 0, 0, int(total)};
     if (lv.ok && bg.sub_log2 > 0) {
-      t.lw = t.lh = bg.sub_log2;
+      int side = bg.sub_log2;
+      // A level with few tasks of many candidates (a coarse level of a small call)
+      // takes 4 x 4 tiles, one MFMA sub-tile each: four times the tasks, each with
+      // about a third of the candidates, so that they do not run long after the other
+      // levels' tasks (the call waits for its longest task).
+      if (bg.small_tiles) {
+        const int64_t t8 = int64_t((lv.w + 7) >> 3) * ((lv.h + 7) >> 3);
+        const int64_t kblocks = int64_t(p.Q) * p.P * 13 / (10 * 64 * t8);  // per 8 x 8 task, expected
+        if (int64_t(p.B) * p.H * t8 < kSmallTileTasks && kblocks >= kSmallTileKBlocks) side = 2;
+      }
+      t.lw = t.lh = side;
       t.ntx = (lv.w + (1 << t.lw) - 1) >> t.lw;
       t.nty = (lv.h + (1 << t.lh) - 1) >> t.lh;
     } else if (lv.ok) {
@@ -1035,14 +1052,14 @@ __device__ inline void zero_grad_value(const Problem& p) {
 }
 
 // Counting (PLACE = false) or placing (PLACE = true) pass of the bucket sort.
-// Workgroup: kBucketThreads * kBucketSamples consecutive samples (q, l, p) of one
+// Workgroup: kBucketThreads * SPT consecutive samples (q, l, p) of one
 // (b, h). `buckets` holds one counter per bucket and (b, h): counts after the count
 // pass, exclusive offsets after the scan, and bucket ends after the place pass.
 // The workgroup first counts its samples per bucket in LDS and publishes each
 // non-empty count with one global atomic; the place pass gets its range of every
 // bucket back from that atomic and hands out slots from it with LDS atomics while
 // it recomputes the keys.
-template <typename TL, bool PLACE>
+template <typename TL, bool PLACE, int SPT>
 __global__ __launch_bounds__(kBucketThreads) void msda_bucket_kernel(const Problem p, const BwdGeom bg,
                                                                      int* __restrict__ buckets,
                                                                      uint32_t* __restrict__ entries,
@@ -1072,7 +1089,8 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket_kernel(const Probl
   int* bucket_row = buckets + int64_t(bh) * nkeys;
   uint32_t* out = entries + int64_t(bh) * bg.region;
   const TL* loc_all = reinterpret_cast<const TL*>(p.loc);
-  const int64_t j0 = int64_t(chunk) * kBucketThreads * kBucketSamples;
+  const int64_t j0 = int64_t(chunk) * kBucketThreads * SPT;
+  constexpr int kBatch = SPT < kBucketBatch ? SPT : kBucketBatch;
 
   // Bucket of sample j of (b, h), or -1 when it is out of range (or j past the end).
   auto key_of = [&](int64_t j) __attribute__((always_inline)) -> int {
@@ -1088,12 +1106,12 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket_kernel(const Probl
 
   if (!in_lds) {
     // Too many buckets for LDS: one global atomic per sample.
-    for (int k = 0; k < kBucketSamples; k += kBucketBatch) {
-      int key[kBucketBatch];
+    for (int k = 0; k < SPT; k += kBatch) {
+      int key[kBatch];
 #pragma unroll
-      for (int i = 0; i < kBucketBatch; ++i) key[i] = key_of(j0 + (k + i) * kBucketThreads + threadIdx.x);
+      for (int i = 0; i < kBatch; ++i) key[i] = key_of(j0 + (k + i) * kBucketThreads + threadIdx.x);
 #pragma unroll
-      for (int i = 0; i < kBucketBatch; ++i) {
+      for (int i = 0; i < kBatch; ++i) {
         if (key[i] < 0) continue;
         const int at = atomicAdd(&bucket_row[key[i]], 1);
         if constexpr (PLACE) out[at] = uint32_t(j0 + (k + i) * kBucketThreads + threadIdx.x);
@@ -1103,12 +1121,12 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket_kernel(const Probl
   }
   for (int k = threadIdx.x; k < nkeys; k += kBucketThreads) hist[k] = 0;
   __syncthreads();
-  for (int k = 0; k < kBucketSamples; k += kBucketBatch) {
-    int key[kBucketBatch];
+  for (int k = 0; k < SPT; k += kBatch) {
+    int key[kBatch];
 #pragma unroll
-    for (int i = 0; i < kBucketBatch; ++i) key[i] = key_of(j0 + (k + i) * kBucketThreads + threadIdx.x);
+    for (int i = 0; i < kBatch; ++i) key[i] = key_of(j0 + (k + i) * kBucketThreads + threadIdx.x);
 #pragma unroll
-    for (int i = 0; i < kBucketBatch; ++i)
+    for (int i = 0; i < kBatch; ++i)
       if (key[i] >= 0) atomicAdd(&hist[key[i]], 1);
   }
   __syncthreads();
@@ -1121,12 +1139,12 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket_kernel(const Probl
   }
   if constexpr (PLACE) {
     __syncthreads();
-    for (int k = 0; k < kBucketSamples; k += kBucketBatch) {
-      int key[kBucketBatch];
+    for (int k = 0; k < SPT; k += kBatch) {
+      int key[kBatch];
 #pragma unroll
-      for (int i = 0; i < kBucketBatch; ++i) key[i] = key_of(j0 + (k + i) * kBucketThreads + threadIdx.x);
+      for (int i = 0; i < kBatch; ++i) key[i] = key_of(j0 + (k + i) * kBucketThreads + threadIdx.x);
 #pragma unroll
-      for (int i = 0; i < kBucketBatch; ++i)
+      for (int i = 0; i < kBatch; ++i)
         if (key[i] >= 0) out[atomicAdd(&hist[key[i]], 1)] = uint32_t(j0 + (k + i) * kBucketThreads + threadIdx.x);
     }
   }
@@ -1175,20 +1193,20 @@ template <> struct KeyWord<4> { using type = u32x4_v; };  // four 32-bit keys
 
 // The bucketing passes for groups of 4 consecutive samples (q, s .. s + 3) of one
 // query and level (L * P and P multiples of 4): one 16- or 32-byte location load and
-// one query / level decode per group. Workgroup: kBucketThreads * kBucketSamples
+// one query / level decode per group. Workgroup: kBucketThreads * SPT
 // consecutive samples of one (b, h), thread t taking groups t, t + 256, ...
 // The count pass publishes per-bucket counts as msda_bucket_kernel does and saves
 // the four keys (16-bit when the keys fit, 0xffff / -1 for out of range) in the
 // grad_value scratch, which nothing else uses before the sort ends; the place pass
 // reads them back and hands out slots.
-template <typename TL, bool PLACE, int KB>
+template <typename TL, bool PLACE, int KB, int SPT>
 __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Problem p, const BwdGeom bg,
                                                                       int* __restrict__ buckets,
                                                                       uint32_t* __restrict__ entries,
                                                                       int chunks_per_bh) {
   using A = typename Elem<TL>::acc;
   using Word = typename KeyWord<KB>::type;
-  constexpr int kGroups = kBucketSamples / 4;  // groups per thread
+  constexpr int kGroups = SPT / 4;  // groups per thread
   __shared__ int scan_sums[kBucketThreads / kWave];
   extern __shared__ __align__(16) unsigned char smem[];
   Level* levels = reinterpret_cast<Level*>(smem);
@@ -2126,6 +2144,7 @@ struct MfmaTile {
   const char* gout;  // grad_out row of (b, q = 0, h)
   uint32_t loc_q, attn_q, gout_q;  // bytes per query step
   int r0, c0, r1, c1;              // tile rows [r0, r1), columns [c0, c1)
+  int nst;                         // sub-tiles the tile has: 4 (8 x 8), or 1 (4 x 4)
   uint32_t ncand;
   FastDiv div_lp;
   int LP;
@@ -2250,7 +2269,7 @@ __device__ inline MfmaCorners mfma_kblock_a(const MfmaTile& t, const Level& lv, 
 }
 
 // TAIL: a tile's last K-blocks, whose second K-step may hold no candidate.
-template <typename T, int NB, bool TAIL = false>
+template <typename T, int NB, int NST, bool TAIL = false>
 __device__ inline void mfma_kblock_b(const MfmaCorners& cr, int lane, const unsigned char* gst, unsigned char* wt,
                                      f32x4_v (&acc)[4][NB], int ksteps = 2) {
   constexpr bool kSplit = sizeof(T) == 4;
@@ -2287,7 +2306,7 @@ __device__ inline void mfma_kblock_b(const MfmaCorners& cr, int lane, const unsi
     }
     const int aoff = i16 * (2 * kMfmaKStep) + g16 * 16;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
+    for (int st = 0; st < NST; ++st) {  // NST = 1: a 4 x 4 tile is sub-tile 0
       const u32x4_v ah = *reinterpret_cast<const u32x4_v*>(wt + st * kMfmaWBytes + aoff);
       const u32x4_v al = *reinterpret_cast<const u32x4_v*>(wt + kMfmaLoTiles + st * kMfmaWBytes + aoff);
 #pragma unroll
@@ -2332,7 +2351,7 @@ __device__ inline int mfma_ksteps(const MfmaTile& t, uint32_t kb) {
 // never waits for younger loads. The main loop issues its loads unconditionally
 // (an entry past the end reads candidate 0), so that the compiler's wait counts
 // stay exact; the last one or two blocks run after it.
-template <typename T, typename TL, int NB, bool SOFTMAX>
+template <typename T, typename TL, int NB, bool SOFTMAX, int NST>
 __device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, const CandRanges& cr,
                                          const uint32_t* __restrict__ ent, int kb0, int kbstep, int lane,
                                          unsigned char* gst, unsigned char* wt, f32x4_v (&acc)[4][NB]) {
@@ -2359,12 +2378,12 @@ __device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, con
     mfma_load_meta<T, TL, SOFTMAX>(t, eb, mb);
     const auto c0 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ma, rows, lane, gst);
     mfma_load_rows<T, NB>(t, eb, lane, rows);
-    mfma_kblock_b<T, NB>(c0, lane, gst, wt, acc);
+    mfma_kblock_b<T, NB, NST>(c0, lane, gst, wt, acc);
     const uint32_t e3 = cand_entry(ent, cr, cand + 3 * step);
     mfma_load_meta<T, TL, SOFTMAX>(t, e2, ma);
     const auto c1 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, mb, rows, lane, gst);
     mfma_load_rows<T, NB>(t, e2, lane, rows);
-    mfma_kblock_b<T, NB>(c1, lane, gst, wt, acc);
+    mfma_kblock_b<T, NB, NST>(c1, lane, gst, wt, acc);
     ea = e2;
     eb = e3;
     cand += 2 * step;
@@ -2375,10 +2394,10 @@ __device__ inline void mfma_tile_kblocks(const MfmaTile& t, const Level& lv, con
     if (two) mfma_load_meta<T, TL, SOFTMAX>(t, eb, mb);
     const auto c0 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb, ea, ma, rows, lane, gst);
     if (two) mfma_load_rows<T, NB>(t, eb, lane, rows);
-    mfma_kblock_b<T, NB, true>(c0, lane, gst, wt, acc, mfma_ksteps(t, kb));
+    mfma_kblock_b<T, NB, NST, true>(c0, lane, gst, wt, acc, mfma_ksteps(t, kb));
     if (two) {
       const auto c1 = mfma_kblock_a<T, TL, NB, SOFTMAX>(t, lv, kb + uint32_t(kbstep), eb, mb, rows, lane, gst);
-      mfma_kblock_b<T, NB, true>(c1, lane, gst, wt, acc, mfma_ksteps(t, kb + uint32_t(kbstep)));
+      mfma_kblock_b<T, NB, NST, true>(c1, lane, gst, wt, acc, mfma_ksteps(t, kb + uint32_t(kbstep)));
     }
   }
 }
@@ -2392,44 +2411,38 @@ __device__ inline void mfma_store_subtile(const Problem& p, const Level& lv, con
                                           int st, const f32x4_v (&c)[NB], int g16, int i16, int accumulate,
                                           T* gv, bool add = false) {
   constexpr int D = 16 * NB;
-  // add: overlapping levels. Tiles of two levels own the shared positions, so each
-  // adds its fp32 sums with one atomic per element (float) or per channel pair
-  // (16-bit: the even lane adds its pair, the odd lane's value taken with a DPP move
-  // before any lane branches): one rounding for the sum and one for the add per
-  // level, where a 16-bit atomic scatter rounds once per contribution.
-  f32x4_v pair[NB];
-  if constexpr (sizeof(T) == 2)
-    if (add)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) pair[nb][r] = quad_perm<kQuadXor1>(c[nb][r]);
+  // add (wave-uniform): overlapping levels. Tiles of two levels own the shared
+  // positions, so each adds its fp32 sums with one atomic per element (float) or per
+  // channel pair (16-bit: the even lane adds its pair, the odd lane's value taken with
+  // a DPP move that every lane runs, before the per-lane bounds test): one rounding
+  // for the sum and one for the add per level, where a 16-bit atomic scatter rounds
+  // once per contribution.
   const int y = t.r0 + 4 * (st >> 1) + g16;
-  if (y >= t.r1) return;
+  const bool yok = y < t.r1;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int x = t.c0 + 4 * (st & 1) + r;
-    if (x < t.c1) {
-      const int64_t pos = int64_t(b) * p.S + lv.start + int64_t(y) * lv.w + x;
-      T* dst = gv + (pos * p.H + h) * D + i16;
+    const bool ok = yok && x < t.c1;
+    const int64_t pos = int64_t(b) * p.S + lv.start + int64_t(y) * lv.w + x;
+    T* dst = gv + (pos * p.H + h) * D + i16;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        if (add) {
-          if constexpr (std::is_same_v<T, float>) {
-            unsafeAtomicAdd(dst + 16 * nb, c[nb][r]);
-          } else if constexpr (std::is_same_v<T, bf16_t>) {
-            if ((i16 & 1) == 0) {
-              const bf16x2_v v2 = {static_cast<__bf16>(c[nb][r]), static_cast<__bf16>(pair[nb][r])};
+    for (int nb = 0; nb < NB; ++nb) {
+      if (add) {
+        if constexpr (std::is_same_v<T, float>) {
+          if (ok) unsafeAtomicAdd(dst + 16 * nb, c[nb][r]);
+        } else {
+          const float pair = quad_perm<kQuadXor1>(c[nb][r]);
+          if (ok && (i16 & 1) == 0) {
+            if constexpr (std::is_same_v<T, bf16_t>) {
+              const bf16x2_v v2 = {static_cast<__bf16>(c[nb][r]), static_cast<__bf16>(pair)};
               __builtin_amdgcn_global_atomic_fadd_v2bf16(reinterpret_cast<bf16x2_v*>(dst + 16 * nb), v2);
-            }
-          } else {
-            if ((i16 & 1) == 0) {
-              const f16x2_v v2 = {static_cast<_Float16>(c[nb][r]), static_cast<_Float16>(pair[nb][r])};
+            } else {
+              const f16x2_v v2 = {static_cast<_Float16>(c[nb][r]), static_cast<_Float16>(pair)};
               __builtin_amdgcn_global_atomic_fadd_v2f16(reinterpret_cast<f16x2_v*>(dst + 16 * nb), v2);
             }
           }
-          continue;
         }
+      } else if (ok) {
         float v = c[nb][r];
         if (accumulate) v += load_acc(dst + 16 * nb);
         store_elem(dst + 16 * nb, v);
@@ -2461,11 +2474,10 @@ __device__ inline void morton_decode(int z, int* x, int* y) {
 }
 
 // The first tile column (or row) of region r of n regions across a level `extent`
-// positions wide with `ntiles` tiles: tile t, centred at position S t + S / 2 (S =
-// the tile side), lies in region floor((S t + S / 2) n / extent).
-__device__ inline int region_first_tile(int r, int n, int extent, int ntiles) {
+// positions wide with `ntiles` tiles of side S: tile t, centred at position
+// S t + S / 2, lies in region floor((S t + S / 2) n / extent).
+__device__ inline int region_first_tile(int r, int n, int extent, int ntiles, int S) {
   if (r >= n) return ntiles;
-  constexpr int S = 1 << kMfmaSubLog2;
   const int64_t num = int64_t(r) * extent - int64_t(S / 2) * n;
   if (num <= 0) return 0;
   const int64_t den = int64_t(S) * n;
@@ -2554,16 +2566,22 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
     int r = 1;
     while (r < kMfmaMaxRegions && 2 * r <= mt) r *= 2;
     grid_s[0] = r;
-    // A tile's expected work goes as 1 / (level area): chunks of the smallest level
-    // hold one task, a level k times larger min(k, kMfmaMaxChunk) tasks.
-    int64_t amin = 0;
+    // A tile's expected work goes as (tile area) / (level area): chunks of the level
+    // with the heaviest tiles hold one task, a level whose tiles expect k times less
+    // work min(k, kMfmaMaxChunk) tasks.
+    int64_t amin = 0, tmin = 1;  // the heaviest tiles' level area over their tile area: amin / tmin
     for (int i = 0; i < p.L; ++i) {
-      const int64_t area = int64_t(levels[i].h) * levels[i].w;
-      if (levels[i].ok && (amin == 0 || area < amin)) amin = area;
+      const int64_t area = int64_t(levels[i].h) * levels[i].w, tarea = int64_t(1) << (lt[i].lh + lt[i].lw);
+      if (levels[i].ok && (amin == 0 || area * tmin < amin * tarea)) {
+        amin = area;
+        tmin = tarea;
+      }
     }
     for (int i = 0; i < p.L; ++i) {
-      const int64_t area = int64_t(levels[order[i]].h) * levels[order[i]].w;
-      csz[i] = int(amin > 0 ? std::max<int64_t>(1, std::min<int64_t>(kMfmaMaxChunk, area / amin)) : 1);
+      const int l = order[i];
+      const int64_t area = int64_t(levels[l].h) * levels[l].w, tarea = int64_t(1) << (lt[l].lh + lt[l].lw);
+      const int64_t k = amin > 0 ? (area * tmin) / (amin * tarea) : 1;
+      csz[i] = int(std::max<int64_t>(1, std::min<int64_t>(kMfmaMaxChunk, k)));
     }
   }
   __syncthreads();
@@ -2594,8 +2612,8 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
         morton_decode(int(pair % (R * R)), &rx, &ry);
         const Level lv = levels[l];
         const LevelTiles tl = lt[l];
-        const int nx = region_first_tile(rx + 1, R, lv.w, tl.ntx) - region_first_tile(rx, R, lv.w, tl.ntx);
-        const int ny = region_first_tile(ry + 1, R, lv.h, tl.nty) - region_first_tile(ry, R, lv.h, tl.nty);
+        const int nx = region_first_tile(rx + 1, R, lv.w, tl.ntx, 1 << tl.lw) - region_first_tile(rx, R, lv.w, tl.ntx, 1 << tl.lw);
+        const int ny = region_first_tile(ry + 1, R, lv.h, tl.nty, 1 << tl.lh) - region_first_tile(ry, R, lv.h, tl.nty, 1 << tl.lh);
         ntab[i] = nx * ny * p.H;
         cnt[j] = (ntab[i] + csz[i % p.L] - 1) / csz[i % p.L];
       }
@@ -2668,9 +2686,9 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
         morton_decode(int(pair % (R * R)), &rx, &ry);
         const Level lvr = levels[l];
         const LevelTiles tlr = lt[l];
-        const int tx0 = region_first_tile(rx, R, lvr.w, tlr.ntx);
-        const int nx = region_first_tile(rx + 1, R, lvr.w, tlr.ntx) - tx0;
-        const int ty0 = region_first_tile(ry, R, lvr.h, tlr.nty);
+        const int tx0 = region_first_tile(rx, R, lvr.w, tlr.ntx, 1 << tlr.lw);
+        const int nx = region_first_tile(rx + 1, R, lvr.w, tlr.ntx, 1 << tlr.lw) - tx0;
+        const int ty0 = region_first_tile(ry, R, lvr.h, tlr.nty, 1 << tlr.lh);
         h = local % p.H;
         const int rest = local / p.H;
         tile = (ty0 + rest / nx) * tlr.ntx + tx0 + rest % nx;
@@ -2716,10 +2734,11 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
       t.loc_q = uint32_t(p.H * LP * 2) * uint32_t(sizeof(TL));
       t.attn_q = uint32_t(p.H * LP * ES);
       t.gout_q = uint32_t(p.H * D * ES);
-      t.r0 = ty << kMfmaSubLog2;
-      t.c0 = tx << kMfmaSubLog2;
-      t.r1 = min(t.r0 + (1 << kMfmaSubLog2), lv.h);
-      t.c1 = min(t.c0 + (1 << kMfmaSubLog2), lv.w);
+      t.r0 = ty << tl.lh;
+      t.c0 = tx << tl.lw;
+      t.r1 = min(t.r0 + (1 << tl.lh), lv.h);
+      t.c1 = min(t.c0 + (1 << tl.lw), lv.w);
+      t.nst = tl.lw < kMfmaSubLog2 ? 1 : 4;  // a 4 x 4 tile is sub-tile 0 alone
       t.ncand = cr.ncand;
       t.div_lp = bg.div_lp;
       t.LP = LP;
@@ -2728,8 +2747,12 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
 
       f32x4_v acc[4][NB];
       // All K-blocks (per-wave mode), or K-blocks wave, wave + 4, ...
-      mfma_tile_kblocks<T, TL, NB, SOFTMAX>(t, lv, cr, ent, per_wave ? 0 : wave, per_wave ? 1 : kMfmaWaves,
-                                            lane, gst, wt, acc);
+      if (t.nst == 1)  // wave-uniform: a 4 x 4 tile runs one sub-tile's MFMAs
+        mfma_tile_kblocks<T, TL, NB, SOFTMAX, 1>(t, lv, cr, ent, per_wave ? 0 : wave, per_wave ? 1 : kMfmaWaves,
+                                                 lane, gst, wt, acc);
+      else
+        mfma_tile_kblocks<T, TL, NB, SOFTMAX, 4>(t, lv, cr, ent, per_wave ? 0 : wave, per_wave ? 1 : kMfmaWaves,
+                                                 lane, gst, wt, acc);
 
       T* gv = reinterpret_cast<T*>(p.grad_value);
       if (per_wave) {
@@ -3110,6 +3133,7 @@ struct BackwardPlan {
   bool bucket;            // try the bucket sort (the kernels re-check on the device)
   size_t bucket_lds;
   int64_t bucket_chunks;  // bucketing workgroups per (b, h)
+  int bucket_spt;         // samples per bucketing thread: kBucketSamples, or kBucketSamplesSmall
   int64_t zero_keys;      // bucket counters to clear per (b, h), at most
   int64_t scan_blocks;    // workgroups of msda_bucket_scan_kernel
   bool mfma;              // grad_value on the matrix cores (8 x 8 tiles)
@@ -3221,9 +3245,13 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   // check the real count, and the VALU owner kernel (which takes 8 x 8 tiles when
   // its capacity is at least 64 positions) runs after the matrix-core one and works
   // only if the counters did not fit.
-  const int64_t mfma_tiles_bound = L * (S / 8 + 1);
+  // A level that takes 4 x 4 tiles (small_tiles) has fewer than kSmallTileTasks / (B H)
+  // 8 x 8 tiles, so fewer than four times that many 4 x 4 ones.
+  const bool small_tiles = !(paths & MSDA_PATH_TILE8);
+  const int64_t small_level_tiles = small_tiles ? 4 * (kSmallTileTasks / std::max<int64_t>(1, B * H) + 1) : 0;
+  const int64_t mfma_tiles_bound = L * std::max<int64_t>(S / 8 + 1, small_level_tiles);
   const int64_t mfma_tiles_estimate =
-      S / 64 + int64_t(ceil(2.5 * sqrt(double(L) * double(S)) / 8.0)) + 2 * L;
+      S / 64 + int64_t(ceil(2.5 * sqrt(double(L) * double(S)) / 8.0)) + 2 * L + (small_tiles ? small_level_tiles : 0);
   const int64_t ls = elem_size(loc_dtype);
   const int64_t per_image = Q * H * std::max(L * P * 2 * ls, D * es);  // 32-bit offsets inside an image
   const bool mfma_sure = 4 * mfma_tiles_bound + kQueueInts <= bg.keys_alloc;
@@ -3244,6 +3272,7 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   plan->mfma = mfma_ok;
   plan->mfma_fallback = mfma_ok && !mfma_sure;
   bg.sub_log2 = mfma_ok ? kMfmaSubLog2 : 0;
+  bg.small_tiles = mfma_ok && small_tiles ? 1 : 0;
   if (mfma_ok) bg.amin = 1 << (2 * kMfmaSubLog2);
   // Tiles per (b, h): every level has at most 3 h w / amin + 1 adaptive tiles.
   const int64_t tiles_bound = mfma_ok ? mfma_tiles_bound : L + 3 * ((L * S + bg.amin - 1) / bg.amin);
@@ -3259,7 +3288,12 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   const int64_t want_keys = std::min<int64_t>(kBucketLdsKeys, plan->zero_keys);
   bg.keys_lds = int(std::max<int64_t>(0, std::min<int64_t>(want_keys, int64_t(budget - std::min(budget, bucket_head)) / 4)));
   plan->bucket_lds = bucket_head + size_t(bg.keys_lds) * 4;
-  plan->bucket_chunks = (samples_bh + kBucketThreads * kBucketSamples - 1) / (kBucketThreads * kBucketSamples);
+  // Small calls (fewer bucketing workgroups than two per CU) give each thread a few
+  // samples, not 32: more workgroups, each a short chain of dependent loads.
+  plan->bucket_spt = kBucketSamples;
+  if (B * H * ((samples_bh + kBucketThreads * kBucketSamples - 1) / (kBucketThreads * kBucketSamples)) < 2 * cus)
+    plan->bucket_spt = kBucketSamplesSmall;
+  plan->bucket_chunks = (samples_bh + kBucketThreads * plan->bucket_spt - 1) / (kBucketThreads * plan->bucket_spt);
   plan->owner_blocks = xcd_group_grid(H, int64_t(bg.nw) * B);
   plan->fallback_nw = int(std::max<int64_t>(1, std::min<int64_t>(bg.nw, (2 * int64_t(cus) + B * H - 1) / (B * H))));
   plan->fallback_blocks = xcd_group_grid(H, int64_t(plan->fallback_nw) * B);
@@ -3373,16 +3407,10 @@ hipError_t launch_owner_mfma(const BackwardPlan& plan, const Problem& p, const i
   return hipErrorInvalidValue;
 }
 
-// The bucket sort: clear the counters, count, scan, place.
-template <typename TL>
-hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* buckets, uint32_t* entries,
-                          hipStream_t st) {
-  {
-    const int64_t n = int64_t(p.B) * p.H * plan.zero_keys;
-    const unsigned blocks = unsigned(std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 1024)));
-    const size_t lds = p.L > kMaxOrderedLevels ? (sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) : 0;
-    hipLaunchKernelGGL(msda_bucket_clear_kernel, dim3(blocks), dim3(256), lds, st, p, plan.bg, buckets);
-  }
+// The count, scan and place passes with SPT samples per bucketing thread.
+template <typename TL, int SPT>
+hipError_t launch_bucket_passes(const BackwardPlan& plan, const Problem& p, int* buckets, uint32_t* entries,
+                                hipStream_t st) {
   const dim3 grid(unsigned(xcd_group_grid(p.H, int64_t(p.B) * plan.bucket_chunks))), block(kBucketThreads);
   const size_t scan_lds = p.L > kMaxOrderedLevels ? (sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) : 0;
   if (plan.bg.group4) {
@@ -3398,11 +3426,12 @@ hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* bucke
                          int(plan.bucket_chunks));
       return hipGetLastError();
     };
-    return plan.bg.key_bytes == 2 ? run(msda_bucket4_kernel<TL, false, 2>, msda_bucket4_kernel<TL, true, 2>)
-                                  : run(msda_bucket4_kernel<TL, false, 4>, msda_bucket4_kernel<TL, true, 4>);
+    return plan.bg.key_bytes == 2
+               ? run(msda_bucket4_kernel<TL, false, 2, SPT>, msda_bucket4_kernel<TL, true, 2, SPT>)
+               : run(msda_bucket4_kernel<TL, false, 4, SPT>, msda_bucket4_kernel<TL, true, 4, SPT>);
   }
-  auto count = msda_bucket_kernel<TL, false>;
-  auto place = msda_bucket_kernel<TL, true>;
+  auto count = msda_bucket_kernel<TL, false, SPT>;
+  auto place = msda_bucket_kernel<TL, true, SPT>;
   hipError_t e = allow_lds(count, plan.bucket_lds);
   if (e == hipSuccess) e = allow_lds(place, plan.bucket_lds);
   if (e != hipSuccess) return e;
@@ -3414,6 +3443,22 @@ hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* bucke
                      int(plan.bucket_chunks));
   return hipGetLastError();
 }
+
+// The bucket sort: clear the counters, count, scan, place.
+template <typename TL>
+hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* buckets, uint32_t* entries,
+                          hipStream_t st) {
+  {
+    const int64_t n = int64_t(p.B) * p.H * plan.zero_keys;
+    const unsigned blocks = unsigned(std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 1024)));
+    const size_t lds = p.L > kMaxOrderedLevels ? (sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) : 0;
+    hipLaunchKernelGGL(msda_bucket_clear_kernel, dim3(blocks), dim3(256), lds, st, p, plan.bg, buckets);
+  }
+  if (plan.bucket_spt == kBucketSamplesSmall)
+    return launch_bucket_passes<TL, kBucketSamplesSmall>(plan, p, buckets, entries, st);
+  return launch_bucket_passes<TL, kBucketSamples>(plan, p, buckets, entries, st);
+}
+
 
 int check_call(int value_dtype, int index_dtype, int loc_dtype, int64_t B, int64_t S, int64_t H,
                int64_t D, int64_t Q, int64_t L, int64_t P, int flags, int allowed_flags) {
@@ -3494,7 +3539,8 @@ const char* msda_last_error(void) { return g_last_error; }
 int msda_abi_version(void) { return MSDA_ABI_VERSION; }
 
 int msda_set_path_override(int paths) {
-  return g_path_override.exchange(paths & (MSDA_PATH_NO_MFMA | MSDA_PATH_ATOMIC_SORT), std::memory_order_relaxed);
+  return g_path_override.exchange(paths & (MSDA_PATH_NO_MFMA | MSDA_PATH_ATOMIC_SORT | MSDA_PATH_TILE8),
+                                  std::memory_order_relaxed);
 }
 
 int msda_launch_geometry(int value_dtype, int64_t batch, int64_t spatial, int64_t heads,

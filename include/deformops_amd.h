@@ -61,6 +61,7 @@ enum msda_flags {
 enum msda_path_bits {
   MSDA_PATH_NO_MFMA = 1,     /* grad_value on the VALU owner kernel instead of the matrix cores */
   MSDA_PATH_ATOMIC_SORT = 2, /* bucket sort publishing counts with global atomics */
+  MSDA_PATH_TILE8 = 4,       /* matrix-core grad_value on 8 x 8 tiles at every level */
 };
 
 /* Return codes. */

@@ -173,9 +173,11 @@ def test_wider_shapes_at_encoder_size(device, sizes, dtype):
 # default for D = 16, 32, 48, 64) and the VALU owner kernel (every other case, float64,
 # and the fallback when the bucket scratch is short), forced by PATH_NO_MFMA; and the
 # two ways the bucket sort publishes its counts: per-workgroup count rows (the default
-# where the scratch has room) or global atomics, forced by PATH_ATOMIC_SORT.
+# where the scratch has room) or global atomics, forced by PATH_ATOMIC_SORT; and the
+# matrix-core kernel's 8 x 8 tiles at every level, forced by PATH_TILE8 (by default
+# levels with few heavy tiles take 4 x 4 tiles: configs 2 and 3 both have such levels).
 
-PATH_BITS = {"mfma": 0, "mfma-atomic-sort": 2, "valu": 1, "valu-atomic-sort": 3}
+PATH_BITS = {"mfma": 0, "mfma-atomic-sort": 2, "mfma-tile8": 4, "valu": 1, "valu-atomic-sort": 3}
 
 
 @pytest.mark.parametrize("path", sorted(PATH_BITS))
