@@ -319,7 +319,8 @@ def _channels_per_lane(dtype: torch.dtype, head_dim: int) -> int:
 def supports_context(context: MSDAContext) -> bool:
     """Whether the HIP kernels take a call with this context.
 
-    A ROCm GPU tensor of float32/float16/bfloat16/float64, at most 64 lanes per
+    A ROCm GPU tensor of float32/float16/bfloat16/float64, an image of fewer than
+    2^31 elements (S * H * D, when S is known), at most 64 lanes per
     head (``D / channels_per_lane``; D <= 512 for 16-bit values) and one unit's
     staged samples, locations and weights within the 64 KiB LDS budget of a wave
     (the library gives a unit more lanes, and a wave fewer units, until a wave
@@ -337,6 +338,10 @@ def supports_context(context: MSDAContext) -> bool:
     head_dim = context.head_dim
     if head_dim == 0:
         return True
+    # The kernels index an image's rows with 32-bit offsets: at most 2^31 - 1 elements
+    # (S H D) per image, the reference's limit (cuda/include/msda_launch.cuh:85-89).
+    if context.num_positions * context.num_heads * head_dim >= 2**31:
+        return False
     lanes = head_dim // _channels_per_lane(context.dtype, head_dim)
     if lanes > 64:  # noqa: PLR2004
         return False

@@ -381,8 +381,9 @@ struct alignas(16) Level {
   int h, w, start, ok;
 };
 
-// A staged sample: four corner byte offsets (inside one batch image, with the
-// unit's head folded in) and four weights (bilinear * attention in the accumulation
+// A staged sample: four corner rows (position * H + head inside one batch image,
+// below 2^31 since the image holds fewer than 2^31 elements; a row is D elements)
+// and four weights (bilinear * attention in the accumulation
 // type, fp32 for every 16-bit value dtype; zero for a corner outside the level). In
 // the backward the weights slot is reused for the reduced G_c once phase 2 has read
 // it.
@@ -450,15 +451,14 @@ __device__ inline void overlap_flag_raise(const Level* levels, int L) {
 template <typename A> struct Geom {
   A dx, dy;
   A w00, w01, w10, w11;  // bilinear weights, zero for corners outside the level
-  uint32_t off[4];
+  uint32_t off[4];       // corner rows of the image: position * H + head (clamped into the level)
   int ix, iy;            // top-left corner (floor of the pixel coordinates), when in
   bool in;               // the sample counts: -1 <= pixel < size on both axes
   bool m00, m01, m10, m11;
 };
 
 template <typename A>
-__device__ inline Geom<A> geometry(A lx, A ly, const Level lv, uint32_t head_bytes,
-                                   uint32_t pos_bytes) {
+__device__ inline Geom<A> geometry(A lx, A ly, const Level lv, uint32_t head, uint32_t heads) {
 #pragma clang fp contract(off)
   Geom<A> g;
   const A W = A(lv.w), H = A(lv.h);
@@ -481,12 +481,12 @@ __device__ inline Geom<A> geometry(A lx, A ly, const Level lv, uint32_t head_byt
   g.m11 = mx1 && my1;
   const int cx0 = max(ix, 0), cx1 = min(ix + 1, lv.w - 1);
   const int cy0 = max(iy, 0), cy1 = min(iy + 1, lv.h - 1);
-  const uint32_t base = uint32_t(lv.start) * pos_bytes + head_bytes;
+  const uint32_t base = uint32_t(lv.start) * heads + head;
   const uint32_t r0 = uint32_t(cy0 * lv.w), r1 = uint32_t(cy1 * lv.w);
-  g.off[0] = base + (r0 + uint32_t(cx0)) * pos_bytes;
-  g.off[1] = base + (r0 + uint32_t(cx1)) * pos_bytes;
-  g.off[2] = base + (r1 + uint32_t(cx0)) * pos_bytes;
-  g.off[3] = base + (r1 + uint32_t(cx1)) * pos_bytes;
+  g.off[0] = base + (r0 + uint32_t(cx0)) * heads;
+  g.off[1] = base + (r0 + uint32_t(cx1)) * heads;
+  g.off[2] = base + (r1 + uint32_t(cx0)) * heads;
+  g.off[3] = base + (r1 + uint32_t(cx1)) * heads;
   const A one(1);
   g.w00 = g.m00 ? (one - g.dx) * (one - g.dy) : A(0);
   g.w01 = g.m01 ? g.dx * (one - g.dy) : A(0);
@@ -604,6 +604,15 @@ __device__ inline UnitRaw copy_unit_records(const Problem& p, const LaneMap& m, 
   return UnitRaw{lds_loc + m.uw * loc_unit, lds_attn + m.uw * attn_unit};
 }
 
+// The address of a lane's channels in row `row` (position * H + head) of an image:
+// 64-bit, so an image may hold up to 2^31 elements (2^33 bytes for float).
+__device__ inline const char* row_at(const char* img, uint32_t row, uint32_t row_bytes, uint32_t lane_bytes) {
+  return img + (uint64_t(row) * row_bytes + lane_bytes);
+}
+__device__ inline char* row_at(char* img, uint32_t row, uint32_t row_bytes, uint32_t lane_bytes) {
+  return img + (uint64_t(row) * row_bytes + lane_bytes);
+}
+
 // Phase 1, shared by both directions: stage every sample of the lane's unit and
 // return the unit's softmax statistics (max and 1 / sum of exp), if any.
 template <typename T, typename TL, bool SOFTMAX>
@@ -631,11 +640,9 @@ __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const L
     sinv = A(1) / sum;
   }
   if (!m.unit_ok) return;
-  const uint32_t pos_bytes = uint32_t(p.H * p.D * ES);
-  const uint32_t head_bytes = uint32_t(m.h * p.D * ES);
   for (int s = m.t; s < LP; s += m.lh) {
     const Geom<A> g = geometry<A>(load_acc(loc + 2 * s), load_acc(loc + 2 * s + 1),
-                                  levels[s / p.P], head_bytes, pos_bytes);
+                                  levels[s / p.P], uint32_t(m.h), uint32_t(p.H));
     A a = load_acc(attn + s);
     if constexpr (SOFTMAX) a = exp_acc(a - smax) * sinv;
     Staged<A> st;
@@ -674,7 +681,7 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
 
   if (!m.unit_ok || m.t * CV >= p.D) return;
   const char* img = p.value + int64_t(m.b) * p.S * p.H * p.D * ES;
-  const uint32_t lane_bytes = uint32_t(m.t * CV * ES);
+  const uint32_t row_bytes = uint32_t(p.D * ES), lane_bytes = uint32_t(m.t * CV * ES);
   A acc[CV];
 #pragma unroll
   for (int i = 0; i < CV; ++i) acc[i] = A(0);
@@ -686,7 +693,7 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_forward_kernel
     const Staged<A> st = wst[s * m.uw_count + m.uw];
     A v[4][CV];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) Chan<T, CV>::load(img + (st.off[c] + lane_bytes), v[c]);
+    for (int c = 0; c < 4; ++c) Chan<T, CV>::load(row_at(img, st.off[c], row_bytes, lane_bytes), v[c]);
 #pragma unroll
     for (int c = 0; c < 4; ++c)
 #pragma unroll
@@ -2802,7 +2809,8 @@ constexpr int kSampleBatch = 2;
 // the lane that staged a sample stores its four.
 template <typename T, int CV, int N>
 __device__ inline void corner_dots(const LaneMap& m, Staged<typename Elem<T>::acc>* wst, int s, bool lane_ok,
-                                   const char* img, uint32_t lane_bytes, const typename Chan<T, CV>::R& g) {
+                                   const char* img, uint32_t row_bytes, uint32_t lane_bytes,
+                                   const typename Chan<T, CV>::R& g) {
   using A = typename Elem<T>::acc;
   using R = typename Chan<T, CV>::R;
   Staged<A> st[N];
@@ -2818,7 +2826,7 @@ __device__ inline void corner_dots(const LaneMap& m, Staged<typename Elem<T>::ac
 #pragma unroll
     for (int n = 0; n < N; ++n)
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v[n][c] = *reinterpret_cast<const R*>(img + (st[n].off[c] + lane_bytes));
+      for (int c = 0; c < 4; ++c) v[n][c] = *reinterpret_cast<const R*>(row_at(img, st[n].off[c], row_bytes, lane_bytes));
 #pragma unroll
     for (int n = 0; n < N; ++n)
 #pragma unroll
@@ -2899,7 +2907,7 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
   const int64_t img_bytes = int64_t(m.b) * p.S * p.H * p.D * ES;
   const char* img = p.value + img_bytes;
   char* gv_img = scatter ? p.grad_value + img_bytes : nullptr;
-  const uint32_t lane_bytes = uint32_t(m.t * CV * ES);
+  const uint32_t row_bytes = uint32_t(p.D * ES), lane_bytes = uint32_t(m.t * CV * ES);
   R g{};
   if (lane_ok) g = *reinterpret_cast<const R*>(p.grad_out + (m.gunit * p.D + m.t * CV) * ES);
   if (gv_img != nullptr && lane_ok) {
@@ -2911,13 +2919,14 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
       const Staged<A> st = wst[s * m.uw_count + m.uw];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
-        if (st.w[c] != A(0)) atomic_add_channels<T, CV>(gv_img + (st.off[c] + lane_bytes), st.w[c], gw);
+        if (st.w[c] != A(0))
+          atomic_add_channels<T, CV>(row_at(gv_img, st.off[c], row_bytes, lane_bytes), st.w[c], gw);
     }
   }
   int s = 0;
   for (; s + kSampleBatch <= LP; s += kSampleBatch)
-    corner_dots<T, CV, kSampleBatch>(m, wst, s, lane_ok, img, lane_bytes, g);
-  for (; s < LP; ++s) corner_dots<T, CV, 1>(m, wst, s, lane_ok, img, lane_bytes, g);
+    corner_dots<T, CV, kSampleBatch>(m, wst, s, lane_ok, img, row_bytes, lane_bytes, g);
+  for (; s < LP; ++s) corner_dots<T, CV, 1>(m, wst, s, lane_ok, img, row_bytes, lane_bytes, g);
   wave_lds_order();  // other lanes of the unit stored some of a sample's sums
 
   // Per-sample location and weight gradients by the lane that staged the sample.
@@ -2925,14 +2934,11 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
   const T* attn = reinterpret_cast<const T*>(raw.attn);
   TL* gloc = reinterpret_cast<TL*>(p.grad_loc) + m.gunit * LP * 2;
   T* gattn = reinterpret_cast<T*>(p.grad_attn) + m.gunit * LP;
-  const uint32_t pos_bytes = uint32_t(p.H * p.D * ES);
-  const uint32_t head_bytes = uint32_t(m.h * p.D * ES);
   A dot(0);
   if (m.unit_ok) {
     for (int s = m.t; s < LP; s += m.lh) {
       const Level lv = levels[s / p.P];
-      const Geom<A> ge = geometry<A>(load_acc(loc + 2 * s), load_acc(loc + 2 * s + 1), lv,
-                                     head_bytes, pos_bytes);
+      const Geom<A> ge = geometry<A>(load_acc(loc + 2 * s), load_acc(loc + 2 * s + 1), lv, 0u, 1u);
       A a = load_acc(attn + s);
       if constexpr (SOFTMAX) a = exp_acc(a - smax) * sinv;
       Staged<A>* slot = wst + s * m.uw_count + m.uw;
@@ -3029,11 +3035,11 @@ int make_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, 
   if (H == 0 || D == 0 || L == 0 || P == 0)
     return fail(MSDA_ERR_INVALID, "msda: heads, channels, levels and points must be positive");
   const int64_t kInt32 = 2147483647;
-  if (S * H * D * es >= kInt32)
+  if (S * H * D >= kInt32)
     return fail(MSDA_ERR_UNSUPPORTED,
-                "msda: one batch image of value holds %lld bytes; the kernels address an image "
-                "with 32-bit offsets and take at most 2^31 - 1 bytes",
-                (long long)(S * H * D * es));
+                "msda: one batch image of value holds %lld elements; the kernels index an image's "
+                "rows with 32-bit offsets and take at most 2^31 - 1 elements",
+                (long long)(S * H * D));
   if (Q * H >= kInt32 || L * P > 4096 || B >= kInt32)
     return fail(MSDA_ERR_UNSUPPORTED, "msda: queries * heads, batch or levels * points too large");
   // Channels per lane: the widest power of two that divides D, fits a 16-byte

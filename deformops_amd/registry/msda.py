@@ -46,7 +46,9 @@ MSDAMethod = Method
 class MSDAContext:
     """What backend selection knows of a call (fields as the reference's,
     registry/msda.py:40-88). ``num_queries`` is left out of equality, and is 0 when
-    symbolic; ``head_dim`` is 0 when unknown."""
+    symbolic; ``head_dim`` is 0 when unknown. ``num_positions`` (S, the value rows of
+    one image; 0 when symbolic or unknown) is this build's own addition, also left out
+    of equality: a backend's addressable image size depends on it."""
 
     device: torch.device
     num_levels: int
@@ -58,6 +60,7 @@ class MSDAContext:
     num_queries: int = dataclasses.field(compare=False)
     method: Method = Method.LINEAR
     head_dim: int = 0
+    num_positions: int = dataclasses.field(default=0, compare=False)
 
     @classmethod
     def from_call(cls, value: Tensor, spatial_shapes: Tensor, sampling_locations: Tensor,
@@ -75,6 +78,7 @@ class MSDAContext:
             num_queries=Q if isinstance(Q, int) else 0,
             method=method,
             head_dim=int(value.shape[3]),
+            num_positions=value.shape[1] if isinstance(value.shape[1], int) else 0,
         )
 
 

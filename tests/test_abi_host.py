@@ -166,6 +166,32 @@ def test_backend_predicate_matches_the_lds_budget(levels, points, dtype, head_di
     assert supports_context(context) is expected
 
 
+@pytest.mark.parametrize("dtype", [0, 2], ids=["f32", "bf16"])
+def test_image_size_limit_is_the_references_element_count(lib, dtype):
+    """An image of S H D = 2^31 - 2 elements (2^31 - 1 is prime) is accepted (the
+    reference's limit is 2^31 - 1 elements whatever the dtype,
+    backends/cuda/include/msda_launch.cuh:85-89), 2^31 are not; the registry's
+    predicate agrees, so such a call is NoBackendError."""
+    from deformops_amd.backends.hip._bridge import supports_context  # noqa: PLC0415
+    from deformops_amd.registry import MSDAContext  # noqa: PLC0415
+
+    for backward in (False, True):
+        assert geometry(lib, dtype, (1, 2**30 - 1, 2, 1, 16, 1, 4), backward)[0] == 0, lib.last_error()
+        assert geometry(lib, dtype, (1, 2**28, 8, 1, 16, 1, 4), backward)[0] == 2  # 2^31 elements
+        assert "2^31 - 1 elements" in lib.last_error()
+    if torch.version.hip is None:
+        pytest.skip("the predicate is for ROCm builds of torch")
+    torch_dtype = torch.float32 if dtype == 0 else torch.bfloat16
+
+    def context(positions: int, heads: int, head_dim: int) -> MSDAContext:
+        return MSDAContext(device=torch.device("cuda"), num_levels=1, num_heads=heads, num_points=4,
+                           dtype=torch_dtype, sm_version=(9, 5), is_training=True, num_queries=16,
+                           head_dim=head_dim, num_positions=positions)
+
+    assert supports_context(context(2**30 - 1, 2, 1))
+    assert not supports_context(context(2**23, 8, 32))
+
+
 def test_missing_library_raises_kernel_error(monkeypatch, tmp_path):
     from deformops_amd.core.errors import KernelNotProvidedError  # noqa: PLC0415
 

@@ -1,18 +1,20 @@
 """The largest image the kernels address, through ``registry.msda``.
 
-The kernels address one batch image of ``value`` (and of ``grad_value``) with 32-bit
-byte offsets, so an image may hold at most 2^31 - 1 bytes (the host rejects larger
-ones; tests/test_abi_host.py). Here one level of 2047 x 2049 = 2^22 - 1 positions
-(bf16) or 889 x 2359 = 2^21 - 1 (float32), with H = 8 and D = 32, makes an image
-512 or 1,024 bytes short of 2^31, and a batch of two puts the second image past
-2^31 bytes. Half the queries sample the first rows of the level and half its last
-rows and columns, where the byte offsets are largest.
+The kernels index the rows of one batch image of ``value`` (and of
+``grad_value``) with 32-bit row offsets (position * H + head) and form 64-bit byte
+addresses from them, so an image may hold up to 2^31 - 1 elements, the reference's
+limit (backends/cuda/include/msda_launch.cuh:85-89); the host rejects larger ones
+(tests/test_abi_host.py). Here one level of 2048 x 4095 positions with H = 8 and
+D = 32 makes an image 2^31 - 524,288 elements: 4.3 GB in bf16 and 8.6 GB in float32,
+past 2^31 bytes either way, and a batch of two puts the second image past 2^32
+bytes. Half the queries sample the first rows of the level and half its last rows
+and columns, where the offsets are largest.
 
 Each group's corners all lie in an 8-row band of the level (or outside the level,
 which the band reproduces: a row beyond the band is beyond the level too). So the
 float64 oracle runs on that band alone, with the band's own level shape: its
 results are those of the full problem, except that the location gradient's y
-component scales with the level height (2047 against 8). grad_value must equal the
+component scales with the level height (2048 against 8). grad_value must equal the
 band's gradient inside each band and be exactly zero everywhere else.
 """
 
@@ -34,14 +36,13 @@ def _pixels(g: torch.Generator, n: int, lo: float, hi: float) -> torch.Tensor:
     return lo + (hi - lo) * torch.rand(n, generator=g, dtype=torch.float64)
 
 
-@pytest.mark.parametrize(("dtype", "shape"), [(torch.bfloat16, (2047, 2049)), (torch.float32, (889, 2359))],
-                         ids=["bf16", "f32"])
-def test_largest_image_addressable_with_32_bit_offsets(device, dtype, shape):
-    Hh, W = shape
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_largest_image_addressable_with_32_bit_row_offsets(device, dtype):
+    Hh, W = 2048, 4095
     B, H, D, P = 2, 8, 32, 4
     S = Hh * W
     es = torch.empty((), dtype=dtype).element_size()
-    assert 0 < 2**31 - S * H * D * es <= 1024
+    assert 0 < 2**31 - S * H * D <= 2**20 and S * H * D * es > 2**31
     Qg = 32  # queries per band
     g = torch.Generator().manual_seed(2047)
     # Pixel coordinates x = loc_x * W - 0.5 (and y alike). Top band rows 0..7: y in
@@ -58,7 +59,7 @@ def test_largest_image_addressable_with_32_bit_offsets(device, dtype, shape):
     loc = torch.cat(locs, 1).to(torch.float32)  # (B, 2 Qg, H, 1, P, 2)
     attn = torch.softmax(torch.randn(B, 2 * Qg, H, P, generator=g, dtype=torch.float64), -1).to(dtype)
     grad_out = torch.randn(B, 2 * Qg, H * D, generator=g, dtype=torch.float64).to(dtype)
-    value = torch.randn(B, S, H, D, device=device, dtype=dtype)  # drawn on the GPU: up to 4.3 GB
+    value = torch.randn(B, S, H, D, device=device, dtype=dtype)  # drawn on the GPU: up to 17 GB
     shapes = torch.tensor([[Hh, W]], device=device)
     starts = torch.tensor([0], device=device)
 
