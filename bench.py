@@ -17,10 +17,12 @@ bracketed by HIP events on that stream) by its algorithmic bytes against 8 TB/s;
 rates the forward kernel's corner gathers against the random-row gather rate of
 L1 and L2 that the row-gather probe (libmsda_probe.so) measures in the same run
 (``l2_peak_128b_rows``: the same probe with 128-byte rows, whole cache lines).
-``roofline.l2_requests`` rates the forward kernel by L2 requests per second, the
-quantity that bounds it: its request count per launch from the counter pass in
-profiles/msda_config4_bf16_l2_requests.md (when that pass ran on the kernel and
-probe sources being measured) over its live call time, against the probe's.
+``roofline.l2_requests`` rates the forward, grad_value and grad_sample kernels by
+L2 requests per second, the quantity that bounds the gathers: each one's request
+count per launch from the counter pass in profiles/msda_config4_bf16_l2_requests.md
+(when that pass ran on the kernel and probe sources being measured) over its live
+time in this run (the forward call; the backward's phases, timed by HIP events the
+library records between them, msda_set_phase_events), against the probe's.
 ``roofline.traffic`` is the HBM bytes of one fwd+bwd from the rocprofv3 counter
 passes in profiles/msda_config4_bf16_hbm_traffic.md, reported only when those
 passes ran on the kernel source being measured. ``cpu_baseline`` times the torch
@@ -64,6 +66,7 @@ PROBE_SOURCE = REPO / "bench_probe" / "gather_probe.hip"
 REQUEST_PROFILE = REPO / "profiles" / "msda_config4_bf16_l2_requests.md"
 PROBE_BYTES = 2048 * 256 * 128 * 8 * 16  # bytes one probe launch gathers (see row_gather_rates)
 SETTLE_S = 0.3  # untimed seconds of the measured work before each timing (see settle_clocks)
+CPU_WARMUP, CPU_TIMED = 2, 5  # iterations of the CPU baseline
 
 
 def _events(n: int) -> list[torch.cuda.Event]:
@@ -176,6 +179,26 @@ def time_calls(w, steps: int, warmup: int, softmax: bool, bwd_flags: int) -> dic
         bwd()
 
     result = {}
+    # The backward's phases (bucket sort, grad_value, grad_sample), from the events the
+    # library records between them (msda_set_phase_events), in their own loop so that
+    # the recording stays out of the other timings.
+    marks = _events(4)
+    for ev in marks:
+        ev.record(stream)
+    torch.cuda.synchronize()
+    lib.set_phase_events([ev.cuda_event for ev in marks])
+    phases: dict[str, list[float]] = {"sort": [], "grad_value": [], "grad_sample": []}
+    try:
+        for i in range(warmup + steps):
+            bwd()
+            marks[3].synchronize()
+            if i >= warmup:
+                for k, name in enumerate(phases):
+                    phases[name].append(marks[k].elapsed_time(marks[k + 1]))
+    finally:
+        lib.set_phase_events(None)
+    for name, times in phases.items():
+        result["phase_" + name] = statistics.mean(times)
     for name, fn in (("forward", fwd), ("backward", bwd), ("fwd_bwd", both)):
         for _ in range(warmup):
             fn()
@@ -294,7 +317,7 @@ def cpu_baseline(config: int, dtype: torch.dtype, loc_dtype: torch.dtype, softma
     (the CPU accumulates 16-bit dtypes in 16 bits).
 
     Sample: batch 1 and at most the first 21,504 queries of the configuration (at
-    config 4, one image: 21,504 of the 86,016 (batch, query) pairs); 1 warm-up and 3
+    config 4, one image: 21,504 of the 86,016 (batch, query) pairs); 2 warm-up and 5
     timed fwd + autograd-bwd iterations, median, scaled by the call's (batch, query)
     pairs over the sample's.
     """
@@ -312,12 +335,12 @@ def cpu_baseline(config: int, dtype: torch.dtype, loc_dtype: torch.dtype, softma
         w = base.to("cpu", dt, lt)
         value, shapes, starts, loc, attn = w.operands(softmax=softmax)
         times = []
-        for i in range(4):
+        for i in range(CPU_WARMUP + CPU_TIMED):
             leaves = [t.detach().clone().requires_grad_(True) for t in (value, loc, attn)]
             t0 = time.perf_counter()
             out = eager_msda(leaves[0], shapes, starts, leaves[1], leaves[2], softmax=softmax)
             out.backward(w.grad_output)
-            if i:
+            if i >= CPU_WARMUP:
                 times.append(time.perf_counter() - t0)
         return statistics.median(times) * 1e3
 
@@ -338,7 +361,8 @@ def cpu_baseline(config: int, dtype: torch.dtype, loc_dtype: torch.dtype, softma
         "sample": (
             f"torch restatement of the reference eager backend (backends/eager/msda_pytorch.py) "
             f"fwd + autograd bwd, {name} (and float32 for value_float32), batch 1 x {sample_queries} queries "
-            f"of config {config} (1/{scale:g} of a call), median of 3 after 1 warm-up, scaled x{scale:g}; "
+            f"of config {config} (1/{scale:g} of a call), median of {CPU_TIMED} after {CPU_WARMUP} warm-up, "
+            f"scaled x{scale:g}; "
             f"torch.set_num_threads({cpu['physical_cores']}) on {cpu['model']}"
         ),
     }
@@ -413,12 +437,22 @@ def main() -> int:
     requests, request_source = profiled_l2_requests() if default else (None, "profiled for the default workload only")
     l2_requests: dict = {"kernel": "msda_forward_kernel", "source": request_source}
     if requests is not None:
-        # Requests per second: the forward's profiled count over its live call time, and
-        # the probe's profiled count over its live launch time (from its GB/s).
-        achieved = requests["msda_forward_kernel"] / (calls["forward"] * 1e-3) / 1e9
+        # Requests per second: each kernel's profiled count over its live time (the
+        # forward call, and the backward's grad_value and grad_sample phases), and the
+        # probe's profiled count over its live launch time (from its GB/s).
         peak = requests["probe_l2"] / (PROBE_BYTES / (gather["l2"] * 1e9)) / 1e9
-        l2_requests.update({"requests_per_launch": requests["msda_forward_kernel"], "achieved": round(achieved, 1),
-                            "peak": round(peak, 1), "unit": "G requests/s", "frac": round(achieved / peak, 4),
+        live = {"msda_forward_kernel": calls["forward"], "msda_grad_value_mfma_kernel": calls["phase_grad_value"],
+                "msda_grad_sample_kernel": calls["phase_grad_sample"]}
+        kernels = {}
+        for kernel, ms in live.items():
+            if kernel in requests:
+                achieved = requests[kernel] / (ms * 1e-3) / 1e9
+                kernels[kernel] = {"requests_per_launch": requests[kernel], "ms": round(ms, 5),
+                                   "achieved": round(achieved, 1), "frac": round(achieved / peak, 4)}
+        forward = kernels["msda_forward_kernel"]
+        l2_requests.update({"requests_per_launch": forward["requests_per_launch"], "achieved": forward["achieved"],
+                            "peak": round(peak, 1), "unit": "G requests/s", "frac": forward["frac"],
+                            "kernels": kernels,
                             "peak_source": "the 2 MiB 64-byte-row probe of this run (one L2 request per row)"})
 
     levels = "/".join(f"{h}x{w_}" for h, w_ in cfg.levels)
@@ -449,11 +483,18 @@ def main() -> int:
             "median_ms_per_step": round(median_ms, 5),
             "forward_call_ms": round(calls["forward"], 5),
             "backward_call_ms": round(calls["backward"], 5),
+            "backward_phase_ms": {name: round(calls["phase_" + name], 5)
+                                  for name in ("sort", "grad_value", "grad_sample")},
             "untimed_settle": settled,
             "device": torch.cuda.get_device_name(device),
         },
         "roofline": {
+            # The contract's roofline is HBM bandwidth (the op is a gather / scatter:
+            # no MFMA-bound formulation). The limit the kernels meet below it is the L2
+            # request rate of their row gathers (forward, grad_sample) and the latency
+            # of grad_value's scattered candidate reads: "binding" and "l2_requests".
             "bound": "hbm",
+            "binding": "l2_request_rate (forward, grad_sample); memory latency (grad_value)",
             "kernel": "one msda_forward + msda_backward C-ABI call pair (forward kernel, bucket sort, "
                       "grad_value, grad_sample), back to back on one stream",
             "achieved": round(call_gbs, 1),

@@ -36,7 +36,7 @@ __all__ = [
 ]
 
 #: MSDA_ABI_VERSION this binding was written for.
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 #: enum msda_dtype.
 DTYPE_CODES: dict[torch.dtype, int] = {
@@ -64,6 +64,7 @@ EXPORTED_SYMBOLS = (
     "msda_abi_version",
     "msda_launch_geometry",
     "msda_set_path_override",
+    "msda_set_phase_events",
 )
 
 _P = ctypes.c_void_p
@@ -101,12 +102,23 @@ class Library:
         lib.msda_launch_geometry.restype = _I
         lib.msda_set_path_override.argtypes = [_I]
         lib.msda_set_path_override.restype = _I
+        lib.msda_set_phase_events.argtypes = [ctypes.POINTER(_P), _I]
+        lib.msda_set_phase_events.restype = _I
         self.forward = lib.msda_forward
         self.backward = lib.msda_backward
 
     def set_path_override(self, paths: int) -> int:
         """Force kernel paths (``PATH_*`` bits, 0 for the library's choice); returns the previous bits."""
         return int(self.cdll.msda_set_path_override(paths))
+
+    def set_phase_events(self, events: list[int] | None) -> None:
+        """Record these four raw HIP events between the phases of later backward calls
+        on this thread (sort, grad_value, grad_sample); ``None`` stops it."""
+        if not events:
+            self.check(self.cdll.msda_set_phase_events(None, 0))
+            return
+        array = (_P * len(events))(*events)
+        self.check(self.cdll.msda_set_phase_events(array, len(events)))
 
     def abi_version(self) -> int:
         return int(self.cdll.msda_abi_version())

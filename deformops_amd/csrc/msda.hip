@@ -3191,6 +3191,17 @@ void device_info(size_t* lds, int* cus) {
 // Kernel paths a test may force (msda_set_path_override), read once per call.
 std::atomic<int> g_path_override{0};
 
+// HIP events msda_backward records between its phases on the calling thread
+// (msda_set_phase_events): before the sort, after it (and the softmax statistics),
+// after grad_value, after grad_sample. Null: none.
+constexpr int kPhaseEvents = 4;
+thread_local hipEvent_t g_phase_events[kPhaseEvents] = {};
+thread_local bool g_phase_events_on = false;
+
+void record_phase(int i, hipStream_t st) {
+  if (g_phase_events_on) (void)hipEventRecord(g_phase_events[i], st);
+}
+
 size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
   const size_t es = size_t(elem_size(dtype));
   const size_t rec = dtype == MSDA_F64 ? sizeof(TileRec<double>) : 8;
@@ -3544,6 +3555,22 @@ const char* msda_last_error(void) { return g_last_error; }
 
 int msda_abi_version(void) { return MSDA_ABI_VERSION; }
 
+int msda_set_phase_events(void* const* events, int count) {
+  g_last_error[0] = '\0';
+  if (count == 0) {
+    g_phase_events_on = false;
+    return MSDA_OK;
+  }
+  if (count != kPhaseEvents || events == nullptr)
+    return fail(MSDA_ERR_INVALID, "msda_set_phase_events: give %d events, or 0 to stop", kPhaseEvents);
+  for (int i = 0; i < kPhaseEvents; ++i) {
+    if (events[i] == nullptr) return fail(MSDA_ERR_INVALID, "msda_set_phase_events: null event %d", i);
+    g_phase_events[i] = static_cast<hipEvent_t>(events[i]);
+  }
+  g_phase_events_on = true;
+  return MSDA_OK;
+}
+
 int msda_set_path_override(int paths) {
   return g_path_override.exchange(paths & (MSDA_PATH_NO_MFMA | MSDA_PATH_ATOMIC_SORT | MSDA_PATH_TILE8),
                                   std::memory_order_relaxed);
@@ -3702,6 +3729,7 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
       value_dtype, loc_dtype == MSDA_F32 && value_dtype != MSDA_F32, plan.sample.cv,
       [&]<typename T, typename TL, int CV>() {
         hipError_t e = hipSuccess;
+        record_phase(0, st);
         // The atomic scatter needs neither the sort nor the owners.
         if (plan.bucket && !atomic_gv) {
           e = launch_buckets<TL>(plan, p, buckets, entries, st);
@@ -3716,6 +3744,7 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
             if (e != hipSuccess) return e;
           }
         }
+        record_phase(1, st);
         if (!accumulate && !plan.mfma && !atomic_gv) {  // the matrix-core kernel zeroes the gaps itself
           const int64_t n = int64_t(p.B) * p.S;
           hipLaunchKernelGGL((msda_gap_zero_kernel<T>), dim3(unsigned((n + 255) / 256)), dim3(256),
@@ -3732,6 +3761,7 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
                       : launch_owner_cvr<T, TL, false>(plan, p, buckets, entries, int(accumulate), after_mfma, st);
         }
         if (e != hipSuccess) return e;
+        record_phase(2, st);
         const dim3 grid(unsigned(plan.sample.num_blocks)), block(unsigned(kWave * plan.sample.waves));
         if (softmax)
           hipLaunchKernelGGL((msda_grad_sample_kernel<T, TL, CV, true>), grid, block,
@@ -3739,7 +3769,9 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
         else
           hipLaunchKernelGGL((msda_grad_sample_kernel<T, TL, CV, false>), grid, block,
                              plan.sample.lds, st, p);
-        return hipGetLastError();
+        e = hipGetLastError();
+        record_phase(3, st);
+        return e;
       });
   if (err != hipSuccess)
     return fail(MSDA_ERR_HIP, "msda_backward: launch failed: %s", hipGetErrorString(err));

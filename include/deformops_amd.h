@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define MSDA_ABI_VERSION 2
+#define MSDA_ABI_VERSION 3
 
 /* Element types. value and attention_weights share one; locations may be
  * MSDA_F32 or the value type (MSDA_F64 only with MSDA_F64 values). */
@@ -163,6 +163,14 @@ int msda_abi_version(void);
  * inputs where another path would be chosen. Results are the same on every path
  * up to rounding. Not meant to be changed while calls run on other threads. */
 int msda_set_path_override(int paths);
+
+/* Makes later msda_backward calls on the calling thread record the four HIP events
+ * events[0..3] (hipEvent_t, created by the caller) on their stream: before the
+ * bucket sort, after the sort (and the softmax statistics), after grad_value, and
+ * after grad_sample; count 0 stops it. No counterpart in the reference: a
+ * measurement hook, so that a benchmark can time each phase of a backward call
+ * (bench.py rates each kernel by its L2 requests per second). */
+int msda_set_phase_events(void* const* events, int count);
 
 /* The launch layout msda_forward / msda_backward would use for these sizes:
  * channels per lane, lanes per (query, head) unit and waves per workgroup. Host
