@@ -131,8 +131,12 @@ def _launch_backward(value: Tensor, shapes: Tensor, starts: Tensor, loc: Tensor,
     grad_loc = torch.empty_like(loc)
     grad_attn = torch.empty_like(attn)
     lib = _lib.load()
+    # The sort's scratch in a workspace of its own (the caching allocator's blocks are
+    # 512-byte aligned), so that the location and weight gradients need not wait for it.
+    workspace = torch.empty(_workspace_bytes(lib, value.dtype, B, Q, H, L, P), dtype=torch.uint8,
+                            device=value.device)
     with _on_device(value.device):
-        status = lib.backward(
+        status = lib.backward_workspace(
             value.data_ptr(), _lib.DTYPE_CODES[value.dtype],
             shapes.data_ptr(), starts.data_ptr(), _lib.INDEX_CODES[shapes.dtype],
             loc.data_ptr(), _lib.DTYPE_CODES[loc.dtype],
@@ -140,10 +144,20 @@ def _launch_backward(value: Tensor, shapes: Tensor, starts: Tensor, loc: Tensor,
             grad_value.data_ptr(), grad_loc.data_ptr(), grad_attn.data_ptr(),
             B, S, H, D, Q, L, P,
             _lib.FLAG_SOFTMAX if softmax else 0,
+            workspace.data_ptr(), workspace.numel(),
             torch._C._cuda_getCurrentRawStream(value.device.index),  # noqa: SLF001
         )
     lib.check(status)
     return grad_value, grad_loc, grad_attn
+
+
+def _workspace_bytes(lib: Any, dtype: torch.dtype, B: int, Q: int, H: int, L: int, P: int) -> int:  # noqa: N803
+    """msda_backward_workspace_size, computed here: the weight gradient's bytes and 4
+    per sample, each rounded up to 256 (a ctypes call per backward would cost more
+    host time than the arithmetic). tests/test_abi_host.py checks it against the library."""
+    del lib
+    samples = B * Q * H * L * P
+    return (samples * dtype.itemsize + 255) // 256 * 256 + (samples * 4 + 255) // 256 * 256
 
 
 def _normalized(value: Tensor, spatial_shapes: Tensor, level_start_index: Tensor, loc: Tensor,

@@ -60,6 +60,8 @@ PATH_TILE8 = 4
 EXPORTED_SYMBOLS = (
     "msda_forward",
     "msda_backward",
+    "msda_backward_workspace",
+    "msda_backward_workspace_size",
     "msda_last_error",
     "msda_abi_version",
     "msda_launch_geometry",
@@ -91,6 +93,11 @@ class Library:
         lib.msda_forward.restype = _I
         lib.msda_backward.argtypes = [_P, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, *([_L] * 7), _I, _P]
         lib.msda_backward.restype = _I
+        lib.msda_backward_workspace.argtypes = [_P, _I, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, *([_L] * 7), _I, _P,
+                                                _L, _P]
+        lib.msda_backward_workspace.restype = _I
+        lib.msda_backward_workspace_size.argtypes = [_I, *([_L] * 7), _I, ctypes.POINTER(_L)]
+        lib.msda_backward_workspace_size.restype = _I
         lib.msda_last_error.argtypes = []
         lib.msda_last_error.restype = ctypes.c_char_p
         lib.msda_abi_version.argtypes = []
@@ -106,6 +113,15 @@ class Library:
         lib.msda_set_phase_events.restype = _I
         self.forward = lib.msda_forward
         self.backward = lib.msda_backward
+        self.backward_workspace = lib.msda_backward_workspace
+
+    def workspace_size(self, dtype: torch.dtype, batch: int, spatial: int, heads: int, channels: int,
+                       queries: int, levels: int, points: int, flags: int = 0) -> int:
+        """Bytes of workspace ``backward_workspace`` takes for these sizes (host only)."""
+        out = _L()
+        self.check(self.cdll.msda_backward_workspace_size(
+            DTYPE_CODES[dtype], batch, spatial, heads, channels, queries, levels, points, flags, ctypes.byref(out)))
+        return int(out.value)
 
     def set_path_override(self, paths: int) -> int:
         """Force kernel paths (``PATH_*`` bits, 0 for the library's choice); returns the previous bits."""

@@ -3547,6 +3547,62 @@ Problem make_problem(const void* value, const void* shapes, const void* starts, 
   return p;
 }
 
+// The backward's workspace: the bucket counters, count rows and softmax statistics
+// (as many bytes as grad_attention_weights, the capacity they have there), then one
+// uint32 sample index per sample. Regions 256-byte aligned.
+struct WorkspaceLayout {
+  int64_t entries_off, total;
+};
+
+WorkspaceLayout workspace_layout(int dtype, int64_t B, int64_t H, int64_t Q, int64_t L, int64_t P) {
+  auto align = [](int64_t v) { return (v + 255) / 256 * 256; };
+  const int64_t samples = B * Q * H * L * P;
+  WorkspaceLayout w;
+  w.entries_off = align(samples * elem_size(dtype));
+  w.total = w.entries_off + align(samples * 4);
+  return w;
+}
+
+// The calling thread's side stream on the current device, and its fork and join
+// events (created on first use and kept: a stream of default priority, events
+// without timing). Per thread, so that a capture on one thread never meets another
+// thread's work.
+// Calls of fewer samples keep one stream: there the fork and join cost about as much
+// as the overlap saves (MI355X: 2.6 us more at 129 K samples, even at 154 K, 5 us
+// less at 1 M, 12-19 us less at 4.6-8.3 M).
+constexpr int64_t kSideStreamSamples = int64_t(1) << 19;
+
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+
+SideStream* side_stream() {
+  thread_local SideStream streams[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  SideStream& s = streams[dev];
+  if (s.stream == nullptr) {
+    if (hipStreamCreateWithFlags(&s.stream, hipStreamNonBlocking) != hipSuccess) return nullptr;
+    if (hipEventCreateWithFlags(&s.fork, hipEventDisableTiming) != hipSuccess ||
+        hipEventCreateWithFlags(&s.join, hipEventDisableTiming) != hipSuccess) {
+      s.stream = nullptr;
+      return nullptr;
+    }
+  }
+  return &s;
+}
+
+template <typename T, typename TL, int CV>
+hipError_t launch_grad_sample(const BackwardPlan& plan, const Problem& p, bool softmax, hipStream_t st) {
+  const dim3 grid(unsigned(plan.sample.num_blocks)), block(unsigned(kWave * plan.sample.waves));
+  if (softmax)
+    hipLaunchKernelGGL((msda_grad_sample_kernel<T, TL, CV, true>), grid, block, plan.sample.lds, st, p);
+  else
+    hipLaunchKernelGGL((msda_grad_sample_kernel<T, TL, CV, false>), grid, block, plan.sample.lds, st, p);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 extern "C" {
@@ -3652,12 +3708,14 @@ int msda_forward(const void* value, int value_dtype, const void* spatial_shapes,
   return MSDA_OK;
 }
 
-int msda_backward(const void* value, int value_dtype, const void* spatial_shapes,
-                  const void* level_start_index, int index_dtype, const void* sampling_locations,
-                  int loc_dtype, const void* attention_weights, const void* grad_output,
-                  void* grad_value, void* grad_sampling_locations, void* grad_attention_weights,
-                  int64_t batch, int64_t spatial, int64_t heads, int64_t channels,
-                  int64_t queries, int64_t levels, int64_t points, int flags, void* stream) {
+// msda_backward (workspace null) and msda_backward_workspace.
+static int backward_call(const void* value, int value_dtype, const void* spatial_shapes,
+                         const void* level_start_index, int index_dtype, const void* sampling_locations,
+                         int loc_dtype, const void* attention_weights, const void* grad_output,
+                         void* grad_value, void* grad_sampling_locations, void* grad_attention_weights,
+                         int64_t batch, int64_t spatial, int64_t heads, int64_t channels,
+                         int64_t queries, int64_t levels, int64_t points, int flags, void* workspace,
+                         int64_t workspace_bytes, void* stream) {
   g_last_error[0] = '\0';
   int rc = check_call(value_dtype, index_dtype, loc_dtype, batch, spatial, heads, channels,
                       queries, levels, points, flags,
@@ -3693,13 +3751,18 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   if (reinterpret_cast<uintptr_t>(grad_sampling_locations) % 4 != 0)
     return fail(MSDA_ERR_INVALID, "msda_backward: grad_sampling_locations must be 4-byte aligned");
   const void* vec[] = {value, grad_output, grad_value, sampling_locations};
+  // The sort's scratch: the caller's workspace when it is large enough (then
+  // grad_sample may run beside the sort), else grad_attention_weights and
+  // grad_sampling_locations (then grad_sample runs last).
+  const WorkspaceLayout wl = workspace_layout(value_dtype, batch, heads, queries, levels, points);
+  const bool use_ws = workspace != nullptr && workspace_bytes >= wl.total && aligned(workspace, 256);
   BackwardPlan plan;
   size_t lds_limit;
   int cus;
   device_info(&lds_limit, &cus);
   rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
-                          loc_dtype, vec, 4, grad_attention_weights, lds_limit, cus, &plan, accumulate,
-                          g_path_override.load(std::memory_order_relaxed));
+                          loc_dtype, vec, 4, use_ws ? workspace : grad_attention_weights, lds_limit, cus, &plan,
+                          accumulate, g_path_override.load(std::memory_order_relaxed));
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,
@@ -3721,14 +3784,32 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
     if (rc != MSDA_OK) return rc;
   }
   // Scratch of the bucket sort: counters in grad_attention_weights, sample indices in
-  // grad_sampling_locations; msda_grad_sample_kernel overwrites both last.
-  int* buckets = static_cast<int*>(grad_attention_weights);
-  uint32_t* entries = static_cast<uint32_t*>(grad_sampling_locations);
+  // grad_sampling_locations, which msda_grad_sample_kernel overwrites last; or the
+  // workspace.
+  int* buckets = static_cast<int*>(use_ws ? workspace : grad_attention_weights);
+  uint32_t* entries = use_ws ? reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + wl.entries_off)
+                             : static_cast<uint32_t*>(grad_sampling_locations);
+  // grad_sample beside the sort: it needs neither the sort nor grad_value, and with
+  // the scratch in the workspace it writes nothing the sort uses. Only where it adds
+  // nothing into grad_value (the matrix-core owners take every level, overlapping ones
+  // included); it joins the caller's stream before the grad_value kernel.
+  SideStream* side = nullptr;
+  if (use_ws && p.sort_overlap && sample_count >= kSideStreamSamples && !g_phase_events_on) {
+    side = side_stream();
+    if (side == nullptr) return fail(MSDA_ERR_HIP, "msda_backward_workspace: no side stream: %s", hipGetErrorString(hipGetLastError()));
+  }
   const bool softmax = flags & MSDA_SOFTMAX;
   const hipError_t err = dispatch(
       value_dtype, loc_dtype == MSDA_F32 && value_dtype != MSDA_F32, plan.sample.cv,
       [&]<typename T, typename TL, int CV>() {
         hipError_t e = hipSuccess;
+        if (side) {  // fork: grad_sample on the side stream, after the caller's prior work
+          e = hipEventRecord(side->fork, st);
+          if (e == hipSuccess) e = hipStreamWaitEvent(side->stream, side->fork, 0);
+          if (e == hipSuccess) e = launch_grad_sample<T, TL, CV>(plan, p, softmax, side->stream);
+          if (e == hipSuccess) e = hipEventRecord(side->join, side->stream);
+          if (e != hipSuccess) return e;
+        }
         record_phase(0, st);
         // The atomic scatter needs neither the sort nor the owners.
         if (plan.bucket && !atomic_gv) {
@@ -3755,27 +3836,68 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
         if (plan.mfma && !atomic_gv)
           e = softmax ? launch_owner_mfma<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
                       : launch_owner_mfma<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
+        if (side) {  // grad_sample done before the owners (whose LDS would keep it from overlapping)
+          e = hipStreamWaitEvent(st, side->join, 0);
+          if (e != hipSuccess) return e;
+        }
         if (e == hipSuccess && !atomic_gv && (!plan.mfma || plan.mfma_fallback)) {
           const int after_mfma = plan.mfma ? 1 : 0;
           e = softmax ? launch_owner_cvr<T, TL, true>(plan, p, buckets, entries, int(accumulate), after_mfma, st)
                       : launch_owner_cvr<T, TL, false>(plan, p, buckets, entries, int(accumulate), after_mfma, st);
         }
-        if (e != hipSuccess) return e;
+        if (e != hipSuccess || side) return e;
         record_phase(2, st);
-        const dim3 grid(unsigned(plan.sample.num_blocks)), block(unsigned(kWave * plan.sample.waves));
-        if (softmax)
-          hipLaunchKernelGGL((msda_grad_sample_kernel<T, TL, CV, true>), grid, block,
-                             plan.sample.lds, st, p);
-        else
-          hipLaunchKernelGGL((msda_grad_sample_kernel<T, TL, CV, false>), grid, block,
-                             plan.sample.lds, st, p);
-        e = hipGetLastError();
+        e = launch_grad_sample<T, TL, CV>(plan, p, softmax, st);
         record_phase(3, st);
         return e;
       });
   if (err != hipSuccess)
     return fail(MSDA_ERR_HIP, "msda_backward: launch failed: %s", hipGetErrorString(err));
   return MSDA_OK;
+}
+
+
+int msda_backward(const void* value, int value_dtype, const void* spatial_shapes,
+                  const void* level_start_index, int index_dtype, const void* sampling_locations,
+                  int loc_dtype, const void* attention_weights, const void* grad_output,
+                  void* grad_value, void* grad_sampling_locations, void* grad_attention_weights,
+                  int64_t batch, int64_t spatial, int64_t heads, int64_t channels,
+                  int64_t queries, int64_t levels, int64_t points, int flags, void* stream) {
+  return backward_call(value, value_dtype, spatial_shapes, level_start_index, index_dtype, sampling_locations,
+                       loc_dtype, attention_weights, grad_output, grad_value, grad_sampling_locations,
+                       grad_attention_weights, batch, spatial, heads, channels, queries, levels, points, flags,
+                       nullptr, 0, stream);
+}
+
+int msda_backward_workspace_size(int value_dtype, int64_t batch, int64_t spatial, int64_t heads,
+                                 int64_t channels, int64_t queries, int64_t levels, int64_t points, int flags,
+                                 int64_t* bytes) {
+  g_last_error[0] = '\0';
+  if (!bytes) return fail(MSDA_ERR_INVALID, "msda_backward_workspace_size: null result pointer");
+  *bytes = 0;
+  if (elem_size(value_dtype) == 0)
+    return fail(MSDA_ERR_INVALID, "msda: unknown value dtype code %d", value_dtype);
+  if (batch < 0 || spatial < 0 || heads < 0 || channels < 0 || queries < 0 || levels < 0 || points < 0)
+    return fail(MSDA_ERR_INVALID, "msda: negative size");
+  (void)spatial;
+  (void)channels;
+  (void)flags;
+  *bytes = workspace_layout(value_dtype, batch, heads, queries, levels, points).total;
+  return MSDA_OK;
+}
+
+int msda_backward_workspace(const void* value, int value_dtype, const void* spatial_shapes,
+                            const void* level_start_index, int index_dtype, const void* sampling_locations,
+                            int loc_dtype, const void* attention_weights, const void* grad_output,
+                            void* grad_value, void* grad_sampling_locations, void* grad_attention_weights,
+                            int64_t batch, int64_t spatial, int64_t heads, int64_t channels,
+                            int64_t queries, int64_t levels, int64_t points, int flags, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+  if (workspace_bytes < 0) return fail(MSDA_ERR_INVALID, "msda_backward_workspace: negative workspace size");
+  return backward_call(value, value_dtype, spatial_shapes, level_start_index, index_dtype, sampling_locations,
+                       loc_dtype, attention_weights, grad_output, grad_value, grad_sampling_locations,
+                       grad_attention_weights, batch, spatial, heads, channels, queries, levels, points, flags,
+                       workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

@@ -91,6 +91,39 @@ def test_invalid_calls_fail_before_any_launch(lib, direction, kwargs, fragment):
         lib.check(rc)
 
 
+def workspace_call(lib, *, vdt=2, sizes=(4, 21504, 8, 32, 21504, 3, 4), flags=0, ws_bytes=0, ptr=1):
+    p = ctypes.c_void_p(ptr) if ptr else None
+    return lib.backward_workspace(p, vdt, p, p, 0, p, 2, p, p, p, p, p, *sizes, flags, p, ws_bytes, None)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
+@pytest.mark.parametrize("sizes", [(4, 21504, 8, 32, 21504, 3, 4), (1, 100, 3, 5, 7, 2, 3), (2, 10, 1, 4, 0, 1, 1)])
+def test_workspace_size_is_the_weight_gradient_and_one_index_per_sample(lib, dtype, sizes):
+    from deformops_amd.backends.hip import _bridge  # noqa: PLC0415
+
+    B, S, H, D, Q, L, P = sizes  # noqa: N806
+    samples = B * Q * H * L * P
+    size = lib.workspace_size(dtype, *sizes)
+    assert size == _bridge._workspace_bytes(lib, dtype, B, Q, H, L, P)  # noqa: SLF001
+    assert size % 256 == 0
+    assert samples * (dtype.itemsize + 4) <= size < samples * (dtype.itemsize + 4) + 512
+    if sizes == (4, 21504, 8, 32, 21504, 3, 4) and dtype == torch.bfloat16:
+        assert size == 49_545_216  # the size the header quotes
+
+
+def test_workspace_calls_validate_like_the_plain_backward(lib):
+    assert workspace_call(lib, ws_bytes=-1) == 1
+    assert "workspace" in lib.cdll.msda_last_error().decode()
+    assert workspace_call(lib, vdt=9) == 1
+    assert "dtype" in lib.cdll.msda_last_error().decode()
+    assert workspace_call(lib, flags=64) == 1
+    assert workspace_call(lib, sizes=(0, 21504, 8, 32, 21504, 3, 4)) == 0
+    out = ctypes.c_int64(7)
+    assert lib.cdll.msda_backward_workspace_size(9, 1, 1, 1, 1, 1, 1, 1, 0, ctypes.byref(out)) == 1
+    assert lib.cdll.msda_backward_workspace_size(2, 1, 1, -1, 1, 1, 1, 1, 0, ctypes.byref(out)) == 1
+    assert lib.cdll.msda_backward_workspace_size(2, 1, 1, 1, 1, 1, 1, 1, 0, None) == 1
+
+
 def test_empty_calls_return_ok_without_a_device(lib):
     assert forward_call(lib, sizes=(0, 21504, 8, 32, 21504, 3, 4)) == 0
     assert forward_call(lib, sizes=(4, 21504, 8, 32, 0, 3, 4)) == 0

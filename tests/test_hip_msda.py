@@ -447,11 +447,66 @@ def test_overlapping_levels_sum_into_grad_value(device, levels, starts, S, dtype
                                  softmax=softmax, dtype=dtype, label=f"overlap {levels} {starts} {path}")
 
 
+def abi_backward(lib, w, grads, flags, stream, workspace=None):
+    """One msda_backward call (workspace None) or msda_backward_workspace call on the
+    workload's operands, writing into ``grads`` = (grad_value, grad_loc, grad_attn)."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    value, shapes, starts, loc, attn = w.operands(softmax=bool(flags & _lib.FLAG_SOFTMAX))
+    B, S, H, D, Q, L, P = w.sizes
+    args = (value.data_ptr(), _lib.DTYPE_CODES[value.dtype], shapes.data_ptr(), starts.data_ptr(),
+            _lib.INDEX_CODES[shapes.dtype], loc.data_ptr(), _lib.DTYPE_CODES[loc.dtype], attn.data_ptr(),
+            w.grad_output.data_ptr(), *(t.data_ptr() for t in grads), B, S, H, D, Q, L, P, flags)
+    if workspace is None:
+        lib.check(lib.backward(*args, stream))
+    else:
+        lib.check(lib.backward_workspace(*args, workspace.data_ptr(), workspace.numel(), stream))
+
+
+def workspace_for(lib, w, flags=0):
+    value = w.value
+    size = lib.workspace_size(value.dtype, *w.sizes, flags)
+    return torch.empty(size, dtype=torch.uint8, device=value.device)
+
+
+@pytest.mark.parametrize("softmax", [False, True], ids=["linear", "softmax"])
+@pytest.mark.parametrize(("cfg", "dtype", "batch", "queries"),
+                         [(4, BF16, None, None), (2, F16, 1, 3000), (3, F32, None, None), (1, F32, None, None)],
+                         ids=["cfg4-bf16", "cfg2-f16", "cfg3-f32", "cfg1-f32"])
+def test_workspace_backward_matches_the_plain_backward(device, cfg, dtype, batch, queries, softmax):
+    """msda_backward_workspace runs grad_sample beside the sort on a side stream: its
+    location and weight gradients are the same kernel's on the same inputs (bit-equal),
+    grad_value the same sums in another order. A workspace one byte short, or
+    misaligned, gives the plain call's schedule with the same results."""
+    from deformops_amd.backends.hip import _lib  # noqa: PLC0415
+
+    lib = _lib.load()
+    kwargs = {k: v for k, v in (("batch", batch), ("queries", queries)) if v is not None}
+    w = make_workload(cfg, **kwargs).to(device, dtype)
+    flags = _lib.FLAG_SOFTMAX if softmax else 0
+    st = torch.cuda.current_stream().cuda_stream
+    plain = [torch.empty_like(t) for t in (w.value, w.sampling_locations, w.attention_weights)]
+    abi_backward(lib, w, plain, flags, st)
+    size = lib.workspace_size(w.value.dtype, *w.sizes, flags)
+    ws = torch.empty(size + 64, dtype=torch.uint8, device=device)  # 512-byte aligned base
+    for workspace in (ws[:size], ws[: size - 1], ws[64:]):
+        got = [torch.full_like(t, float("nan")) for t in plain]
+        ws.fill_(255)  # the workspace's contents must not matter
+        abi_backward(lib, w, got, flags, st, workspace=workspace)
+        torch.cuda.synchronize()
+        assert rel_err(got[0], plain[0].double().cpu()) <= BWD_TOL[dtype]
+        torch.testing.assert_close(got[1], plain[1], rtol=0, atol=0)
+        torch.testing.assert_close(got[2], plain[2], rtol=0, atol=0)
+
+
+@pytest.mark.parametrize("entry", ["plain", "workspace"])
 @pytest.mark.parametrize("dtype", [BF16, F32], ids=["bf16", "f32"])
-def test_calls_replay_from_a_hip_graph(device, dtype):
+def test_calls_replay_from_a_hip_graph(device, dtype, entry):
     """The forward and backward C-ABI calls launch kernels only (no allocation, no
-    memset), so a caller can capture them in a HIP graph. Each replay, with eager
-    work in between that poisons the outputs, must give the eager results."""
+    memset), so a caller can capture them in a HIP graph; the workspace backward's
+    fork onto its side stream and join back are captured as graph edges. Each
+    replay, with eager work in between that poisons the outputs, must give the
+    eager results."""
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
 
     lib = _lib.load()
@@ -461,16 +516,14 @@ def test_calls_replay_from_a_hip_graph(device, dtype):
     codes = (_lib.DTYPE_CODES[value.dtype], _lib.DTYPE_CODES[loc.dtype], _lib.INDEX_CODES[shapes.dtype])
     out = torch.empty((B, Q, H * D), dtype=dtype, device=device)
     gv, gl, ga = torch.empty_like(value), torch.empty_like(loc), torch.empty_like(attn)
+    ws = workspace_for(lib, w, _lib.FLAG_SOFTMAX) if entry == "workspace" else None
 
     def calls() -> None:
         st = torch.cuda.current_stream().cuda_stream
         lib.check(lib.forward(value.data_ptr(), codes[0], shapes.data_ptr(), starts.data_ptr(), codes[2],
                               loc.data_ptr(), codes[1], attn.data_ptr(), out.data_ptr(),
                               B, S, H, D, Q, L, P, _lib.FLAG_SOFTMAX, st))
-        lib.check(lib.backward(value.data_ptr(), codes[0], shapes.data_ptr(), starts.data_ptr(), codes[2],
-                               loc.data_ptr(), codes[1], attn.data_ptr(), w.grad_output.data_ptr(),
-                               gv.data_ptr(), gl.data_ptr(), ga.data_ptr(),
-                               B, S, H, D, Q, L, P, _lib.FLAG_SOFTMAX, st))
+        abi_backward(lib, w, (gv, gl, ga), _lib.FLAG_SOFTMAX, st, workspace=ws)
 
     calls()
     torch.cuda.synchronize()
@@ -489,6 +542,8 @@ def test_calls_replay_from_a_hip_graph(device, dtype):
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
+        if ws is not None:
+            ws.fill_(255)
         for got, want in zip((out, gv, gl, ga), eager):
             assert not torch.isnan(got).any()
             # grad_value's summation order may differ between runs; the rest is exact.
@@ -496,10 +551,12 @@ def test_calls_replay_from_a_hip_graph(device, dtype):
             assert rel_err(got, want.double().cpu()) <= tol
 
 
-def test_concurrent_calls_from_two_threads_on_two_streams(device):
-    """The library keeps no state between calls (scratch lives in each call's outputs,
-    errors are thread-local): two host threads, each calling the backward on its own
-    stream with its own workload, get the sequential results."""
+@pytest.mark.parametrize("entry", ["plain", "workspace"])
+def test_concurrent_calls_from_two_threads_on_two_streams(device, entry):
+    """The library keeps no state between calls (scratch lives in each call's outputs
+    or workspace, side streams and errors are per thread): two host threads, each
+    calling the backward on its own stream with its own workload, get the sequential
+    results."""
     import threading  # noqa: PLC0415
 
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
@@ -508,15 +565,10 @@ def test_concurrent_calls_from_two_threads_on_two_streams(device):
     works = [make_workload(2, batch=1, queries=1800, seed=s).to(device, dt) for s, dt in ((1, BF16), (2, F32))]
 
     def backward(w, stream):
-        value, shapes, starts, loc, attn = w.operands()
-        B, S, H, D, Q, L, P = w.sizes
-        gv, gl, ga = torch.empty_like(value), torch.empty_like(loc), torch.empty_like(attn)
-        lib.check(lib.backward(value.data_ptr(), _lib.DTYPE_CODES[value.dtype], shapes.data_ptr(),
-                               starts.data_ptr(), _lib.INDEX_CODES[shapes.dtype], loc.data_ptr(),
-                               _lib.DTYPE_CODES[loc.dtype], attn.data_ptr(), w.grad_output.data_ptr(),
-                               gv.data_ptr(), gl.data_ptr(), ga.data_ptr(), B, S, H, D, Q, L, P, 0,
-                               stream.cuda_stream))
-        return gv, gl, ga
+        grads = [torch.empty_like(t) for t in (w.value, w.sampling_locations, w.attention_weights)]
+        ws = workspace_for(lib, w) if entry == "workspace" else None
+        abi_backward(lib, w, grads, 0, stream.cuda_stream, workspace=ws)
+        return grads
 
     stream0 = torch.cuda.current_stream()
     expected = [backward(w, stream0) for w in works]
