@@ -447,7 +447,7 @@ def test_overlapping_levels_sum_into_grad_value(device, levels, starts, S, dtype
                                  softmax=softmax, dtype=dtype, label=f"overlap {levels} {starts} {path}")
 
 
-def abi_backward(lib, w, grads, flags, stream, workspace=None):
+def abi_backward_into(lib, w, grads, flags, stream, workspace=None):
     """One msda_backward call (workspace None) or msda_backward_workspace call on the
     workload's operands, writing into ``grads`` = (grad_value, grad_loc, grad_attn)."""
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
@@ -486,13 +486,13 @@ def test_workspace_backward_matches_the_plain_backward(device, cfg, dtype, batch
     flags = _lib.FLAG_SOFTMAX if softmax else 0
     st = torch.cuda.current_stream().cuda_stream
     plain = [torch.empty_like(t) for t in (w.value, w.sampling_locations, w.attention_weights)]
-    abi_backward(lib, w, plain, flags, st)
+    abi_backward_into(lib, w, plain, flags, st)
     size = lib.workspace_size(w.value.dtype, *w.sizes, flags)
     ws = torch.empty(size + 64, dtype=torch.uint8, device=device)  # 512-byte aligned base
     for workspace in (ws[:size], ws[: size - 1], ws[64:]):
         got = [torch.full_like(t, float("nan")) for t in plain]
         ws.fill_(255)  # the workspace's contents must not matter
-        abi_backward(lib, w, got, flags, st, workspace=workspace)
+        abi_backward_into(lib, w, got, flags, st, workspace=workspace)
         torch.cuda.synchronize()
         assert rel_err(got[0], plain[0].double().cpu()) <= BWD_TOL[dtype]
         torch.testing.assert_close(got[1], plain[1], rtol=0, atol=0)
@@ -523,7 +523,7 @@ def test_calls_replay_from_a_hip_graph(device, dtype, entry):
         lib.check(lib.forward(value.data_ptr(), codes[0], shapes.data_ptr(), starts.data_ptr(), codes[2],
                               loc.data_ptr(), codes[1], attn.data_ptr(), out.data_ptr(),
                               B, S, H, D, Q, L, P, _lib.FLAG_SOFTMAX, st))
-        abi_backward(lib, w, (gv, gl, ga), _lib.FLAG_SOFTMAX, st, workspace=ws)
+        abi_backward_into(lib, w, (gv, gl, ga), _lib.FLAG_SOFTMAX, st, workspace=ws)
 
     calls()
     torch.cuda.synchronize()
@@ -567,7 +567,7 @@ def test_concurrent_calls_from_two_threads_on_two_streams(device, entry):
     def backward(w, stream):
         grads = [torch.empty_like(t) for t in (w.value, w.sampling_locations, w.attention_weights)]
         ws = workspace_for(lib, w) if entry == "workspace" else None
-        abi_backward(lib, w, grads, 0, stream.cuda_stream, workspace=ws)
+        abi_backward_into(lib, w, grads, 0, stream.cuda_stream, workspace=ws)
         return grads
 
     stream0 = torch.cuda.current_stream()
