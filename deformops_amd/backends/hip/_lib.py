@@ -36,7 +36,7 @@ __all__ = [
 ]
 
 #: MSDA_ABI_VERSION this binding was written for.
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 #: enum msda_dtype.
 DTYPE_CODES: dict[torch.dtype, int] = {
@@ -62,6 +62,7 @@ EXPORTED_SYMBOLS = (
     "msda_backward",
     "msda_backward_workspace",
     "msda_backward_workspace_size",
+    "msda_backward_no_alloc",
     "msda_last_error",
     "msda_abi_version",
     "msda_launch_geometry",
@@ -98,6 +99,8 @@ class Library:
         lib.msda_backward_workspace.restype = _I
         lib.msda_backward_workspace_size.argtypes = [_I, *([_L] * 7), _I, ctypes.POINTER(_L)]
         lib.msda_backward_workspace_size.restype = _I
+        lib.msda_backward_no_alloc.argtypes = lib.msda_backward.argtypes
+        lib.msda_backward_no_alloc.restype = _I
         lib.msda_last_error.argtypes = []
         lib.msda_last_error.restype = ctypes.c_char_p
         lib.msda_abi_version.argtypes = []
@@ -114,6 +117,7 @@ class Library:
         self.forward = lib.msda_forward
         self.backward = lib.msda_backward
         self.backward_workspace = lib.msda_backward_workspace
+        self.backward_no_alloc = lib.msda_backward_no_alloc
 
     def workspace_size(self, dtype: torch.dtype, batch: int, spatial: int, heads: int, channels: int,
                        queries: int, levels: int, points: int, flags: int = 0) -> int:

@@ -3605,6 +3605,47 @@ hipError_t launch_grad_sample(const BackwardPlan& plan, const Problem& p, bool s
 
 }  // namespace
 
+// The scratch of msda_backward_no_alloc: the workspace msda_backward_workspace takes,
+// as a device array the code object brings (no allocation at call time). Each device
+// holds its own copy from the module's load on that device until the process ends.
+// 64 MiB holds the workspace of every batch of 2^23 samples or fewer in any dtype up
+// to 4 bytes (B = 4, Q = 21,504, H = 8, L = 3, P = 4: 66,060,288 bytes in float32).
+constexpr int64_t kScratchBytes = int64_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+// `scratch` in host code is the host-side shadow of the device array, not a device
+// address: the device address comes from hipGetSymbolAddress, once per device with
+// that device current, and is kept.
+struct ScratchSlot {
+  std::atomic<void*> addr{nullptr};
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return fail(MSDA_ERR_HIP, "msda_backward_no_alloc: no current device: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MSDA_ERR_INVALID, "msda_backward_no_alloc: device %d beyond the %d the library tracks", dev,
+                kMaxDevices);
+  void* addr = g_scratch[dev].addr.load(std::memory_order_acquire);
+  if (addr == nullptr) {
+    // Concurrent first calls on one device look up the same address.
+    e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || addr == nullptr)
+      return fail(MSDA_ERR_HIP, "msda_backward_no_alloc: hipGetSymbolAddress(scratch) failed: %s",
+                  hipGetErrorString(e));
+    g_scratch[dev].addr.store(addr, std::memory_order_release);
+  }
+  *out = addr;
+  return MSDA_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* msda_last_error(void) { return g_last_error; }
@@ -3715,7 +3756,7 @@ static int backward_call(const void* value, int value_dtype, const void* spatial
                          void* grad_value, void* grad_sampling_locations, void* grad_attention_weights,
                          int64_t batch, int64_t spatial, int64_t heads, int64_t channels,
                          int64_t queries, int64_t levels, int64_t points, int flags, void* workspace,
-                         int64_t workspace_bytes, void* stream) {
+                         int64_t workspace_bytes, bool fork, void* stream) {
   g_last_error[0] = '\0';
   int rc = check_call(value_dtype, index_dtype, loc_dtype, batch, spatial, heads, channels,
                       queries, levels, points, flags,
@@ -3794,7 +3835,7 @@ static int backward_call(const void* value, int value_dtype, const void* spatial
   // nothing into grad_value (the matrix-core owners take every level, overlapping ones
   // included); it joins the caller's stream before the grad_value kernel.
   SideStream* side = nullptr;
-  if (use_ws && p.sort_overlap && sample_count >= kSideStreamSamples && !g_phase_events_on) {
+  if (fork && use_ws && p.sort_overlap && sample_count >= kSideStreamSamples && !g_phase_events_on) {
     side = side_stream();
     if (side == nullptr) return fail(MSDA_ERR_HIP, "msda_backward_workspace: no side stream: %s", hipGetErrorString(hipGetLastError()));
   }
@@ -3866,7 +3907,7 @@ int msda_backward(const void* value, int value_dtype, const void* spatial_shapes
   return backward_call(value, value_dtype, spatial_shapes, level_start_index, index_dtype, sampling_locations,
                        loc_dtype, attention_weights, grad_output, grad_value, grad_sampling_locations,
                        grad_attention_weights, batch, spatial, heads, channels, queries, levels, points, flags,
-                       nullptr, 0, stream);
+                       nullptr, 0, false, stream);
 }
 
 int msda_backward_workspace_size(int value_dtype, int64_t batch, int64_t spatial, int64_t heads,
@@ -3897,7 +3938,33 @@ int msda_backward_workspace(const void* value, int value_dtype, const void* spat
   return backward_call(value, value_dtype, spatial_shapes, level_start_index, index_dtype, sampling_locations,
                        loc_dtype, attention_weights, grad_output, grad_value, grad_sampling_locations,
                        grad_attention_weights, batch, spatial, heads, channels, queries, levels, points, flags,
-                       workspace, workspace_bytes, stream);
+                       workspace, workspace_bytes, true, stream);
+}
+
+int msda_backward_no_alloc(const void* value, int value_dtype, const void* spatial_shapes,
+                           const void* level_start_index, int index_dtype, const void* sampling_locations,
+                           int loc_dtype, const void* attention_weights, const void* grad_output,
+                           void* grad_value, void* grad_sampling_locations, void* grad_attention_weights,
+                           int64_t batch, int64_t spatial, int64_t heads, int64_t channels,
+                           int64_t queries, int64_t levels, int64_t points, int flags, void* stream) {
+  g_last_error[0] = '\0';
+  int rc = check_call(value_dtype, index_dtype, loc_dtype, batch, spatial, heads, channels,
+                      queries, levels, points, flags,
+                      MSDA_SOFTMAX | MSDA_ACCUMULATE_GRAD_VALUE | MSDA_GRAD_VALUE_ATOMIC);
+  if (rc != MSDA_OK) return rc;
+  const int64_t need = workspace_layout(value_dtype, batch, heads, queries, levels, points).total;
+  if (need > kScratchBytes)
+    return fail(MSDA_ERR_INVALID,
+                "msda_backward_no_alloc: these sizes need %lld bytes of scratch, the static scratch holds %lld "
+                "(use msda_backward_workspace)",
+                static_cast<long long>(need), static_cast<long long>(kScratchBytes));
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc != MSDA_OK) return rc;
+  return backward_call(value, value_dtype, spatial_shapes, level_start_index, index_dtype, sampling_locations,
+                       loc_dtype, attention_weights, grad_output, grad_value, grad_sampling_locations,
+                       grad_attention_weights, batch, spatial, heads, channels, queries, levels, points, flags,
+                       ws, kScratchBytes, false, stream);
 }
 
 }  // extern "C"

@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define MSDA_ABI_VERSION 3
+#define MSDA_ABI_VERSION 4
 
 /* Element types. value and attention_weights share one; locations may be
  * MSDA_F32 or the value type (MSDA_F64 only with MSDA_F64 values). */
@@ -187,6 +187,30 @@ int msda_backward_workspace(const void* value, int value_dtype,
 int msda_backward_workspace_size(int value_dtype, int64_t batch, int64_t spatial, int64_t heads,
                                  int64_t channels, int64_t queries, int64_t levels, int64_t points,
                                  int flags, int64_t* bytes);
+
+/*
+ * msda_backward_workspace with the workspace in a static device array of 64 MiB
+ * (`scratch` in msda.hip, one per device, held from the module's load on that device
+ * until the process ends): a backward that allocates nothing, for callers that cannot
+ * call hipMalloc (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid allocation). No counterpart in the reference. Same arguments and results as
+ * msda_backward, kernels in turn on `stream` (no side stream). Sizes whose workspace
+ * exceeds 64 MiB (msda_backward_workspace_size; more than 2^23 samples in 4-byte
+ * dtypes) fail with MSDA_ERR_INVALID before any launch. Every call on a device shares
+ * that device's array, so calls that overlap on one device (two streams, two threads)
+ * race and give wrong gradients: serialize them.
+ */
+int msda_backward_no_alloc(const void* value, int value_dtype,
+                           const void* spatial_shapes, const void* level_start_index,
+                           int index_dtype,
+                           const void* sampling_locations, int loc_dtype,
+                           const void* attention_weights,
+                           const void* grad_output,
+                           void* grad_value, void* grad_sampling_locations,
+                           void* grad_attention_weights,
+                           int64_t batch, int64_t spatial, int64_t heads, int64_t channels,
+                           int64_t queries, int64_t levels, int64_t points,
+                           int flags, void* stream);
 
 /* The message of the calling thread's last failed call ("" if none). Replaces the
  * std::runtime_error text of TORCH_CHECK (include/stable_compat.cuh:33-46). */
