@@ -21,6 +21,7 @@ by its one owner and stored once. ``chunk_step``, ``channels_per_thread`` and
 from __future__ import annotations
 
 import contextlib
+import functools
 from typing import Any
 
 import torch
@@ -133,7 +134,7 @@ def _launch_backward(value: Tensor, shapes: Tensor, starts: Tensor, loc: Tensor,
     lib = _lib.load()
     # The sort's scratch in a workspace of its own (the caching allocator's blocks are
     # 512-byte aligned), so that the location and weight gradients need not wait for it.
-    workspace = torch.empty(_workspace_bytes(lib, value.dtype, B, Q, H, L, P), dtype=torch.uint8,
+    workspace = torch.empty(_workspace_bytes(value.dtype, B, S, H, Q, L, P), dtype=torch.uint8,
                             device=value.device)
     with _on_device(value.device):
         status = lib.backward_workspace(
@@ -151,13 +152,10 @@ def _launch_backward(value: Tensor, shapes: Tensor, starts: Tensor, loc: Tensor,
     return grad_value, grad_loc, grad_attn
 
 
-def _workspace_bytes(lib: Any, dtype: torch.dtype, B: int, Q: int, H: int, L: int, P: int) -> int:  # noqa: N803
-    """msda_backward_workspace_size, computed here: the weight gradient's bytes and 4
-    per sample, each rounded up to 256 (a ctypes call per backward would cost more
-    host time than the arithmetic). tests/test_abi_host.py checks it against the library."""
-    del lib
-    samples = B * Q * H * L * P
-    return (samples * dtype.itemsize + 255) // 256 * 256 + (samples * 4 + 255) // 256 * 256
+@functools.lru_cache(maxsize=256)
+def _workspace_bytes(dtype: torch.dtype, B: int, S: int, H: int, Q: int, L: int, P: int) -> int:  # noqa: N803
+    """msda_backward_workspace_size for these sizes, asked of the library once per shape."""
+    return _lib.load().workspace_size(dtype, B, S, H, 0, Q, L, P)
 
 
 def _normalized(value: Tensor, spatial_shapes: Tensor, level_start_index: Tensor, loc: Tensor,

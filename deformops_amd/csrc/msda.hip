@@ -766,6 +766,8 @@ constexpr int kTargetRecords = 8192;
 constexpr int kSmallTileTasks = 384;
 constexpr int kSmallTileKBlocks = 24;
 constexpr int kBucketLdsKeys = 8192;  // LDS bucket counters of the bucketing kernels (32 KB)
+// Samples per (b, h) up to which the sort runs in one launch (msda_bucket_small_kernel).
+constexpr int64_t kSmallSortSamples = int64_t(1) << 14;
 constexpr int kMaxOrderedLevels = 64;
 // Scratch ints after the bucket rows for the matrix-core kernel's kXcds work-queue
 // counters, each on its own 128-byte line (plus the slack to align the first).
@@ -1194,6 +1196,27 @@ __device__ inline void group_slots(const int (&key)[4], Cursor* cur, int (&slot)
   }
 }
 
+// The four keys of the sample group whose eight coordinates start at `lc` (one
+// 16-byte load for 16-bit locations, eight loads for float ones), at level lv.
+template <typename TL>
+__device__ inline void group_keys(const char* lc, const Level& lv, const LevelTiles& tl, int (&k)[4]) {
+  using A = typename Elem<TL>::acc;
+  A xy[8];
+  if constexpr (sizeof(TL) == 2) {
+    const u32x4_v w = *reinterpret_cast<const u32x4_v*>(lc);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xy[2 * i] = Chan16<TL, 2>::lo(w[i]);
+      xy[2 * i + 1] = Chan16<TL, 2>::hi(w[i]);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xy[i] = load_acc(reinterpret_cast<const TL*>(lc) + i);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) k[i] = sample_key<A>(xy[2 * i], xy[2 * i + 1], lv, tl);
+}
+
 template <int N> struct KeyWord;
 template <> struct KeyWord<2> { using type = u32x2_v; };  // four 16-bit keys
 template <> struct KeyWord<4> { using type = u32x4_v; };  // four 32-bit keys
@@ -1254,23 +1277,7 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
     const uint32_t g32 = uint32_t(g);
     const uint32_t q = fdiv(g32, bg.div_gpq), r = g32 - q * gpq;
     const int l = int(fdiv(r, bg.div_gpl));
-    const char* lc = loc_bh + (q * loc_q + r * uint32_t(8 * sizeof(TL)));
-    A xy[8];
-    if constexpr (sizeof(TL) == 2) {
-      const u32x4_v w = *reinterpret_cast<const u32x4_v*>(lc);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        xy[2 * i] = Chan16<TL, 2>::lo(w[i]);
-        xy[2 * i + 1] = Chan16<TL, 2>::hi(w[i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) xy[i] = load_acc(reinterpret_cast<const TL*>(lc) + i);
-    }
-    const Level lv = levels[l];
-    const LevelTiles tl = lt[l];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) k[i] = sample_key<A>(xy[2 * i], xy[2 * i + 1], lv, tl);
+    group_keys<TL>(loc_bh + (q * loc_q + r * uint32_t(8 * sizeof(TL))), levels[l], lt[l], k);
   };
   auto save = [&](int64_t g, const int (&k)[4]) __attribute__((always_inline)) {
     if (g >= ngroups || !keep_keys) return;
@@ -1401,6 +1408,100 @@ __global__ __launch_bounds__(kBucketThreads) void msda_bucket4_kernel(const Prob
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         if (key[i][c] >= 0) out[slot[c]] = uint32_t(4 * g + c);
+    }
+  }
+}
+
+// The whole bucket sort of a small call in one launch: workgroup (b, h) counts its
+// Q L P samples (in groups of 4, as msda_bucket4_kernel), scans the counts and places
+// the samples, with the counters in LDS (or, when they do not fit there, in its own
+// row of the scratch, which no other workgroup touches). No clear launch, no count
+// rows and no second pass over the scratch: one launch where the general sort takes
+// four, for calls whose (b, h) hold few samples. The bucket rows end up as the
+// general sort leaves them (bucket ends), and workgroup 0 clears the matrix-core
+// kernel's queue counters. Grid: B H workgroups.
+constexpr int kSmallSortThreads = 1024;
+constexpr int kSmallSortBatch = 4;  // groups per thread whose locations load together
+template <typename TL>
+__global__ __launch_bounds__(kSmallSortThreads) void msda_bucket_small_kernel(const Problem p, const BwdGeom bg,
+                                                                             int* __restrict__ buckets,
+                                                                             uint32_t* __restrict__ entries,
+                                                                             int lds_keys) {
+  __shared__ int scan_sums[kSmallSortThreads / kWave];
+  extern __shared__ __align__(16) unsigned char smem[];
+  Level* levels = reinterpret_cast<Level*>(smem);
+  LevelTiles* lt = reinterpret_cast<LevelTiles*>(smem + sizeof(Level) * size_t(p.L));
+  const size_t head = ((sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) + 15) & ~size_t(15);
+  int64_t* total = reinterpret_cast<int64_t*>(smem + head);
+  int* hist = reinterpret_cast<int*>(smem + head + 16);
+  bool overlap = false;
+  const int64_t ntiles = load_tiles(p, bg, levels, lt, total, &overlap);
+  const int64_t nkeys = 4 * ntiles;
+  if (ntiles < 0 || nkeys > bg.keys_alloc) return;  // no bucketing: the owners scan
+  if (overlap && p.zero_gv) zero_grad_value(p);
+  const int bh = int(blockIdx.x), b = bh / p.H, h = bh - b * p.H;
+  const int T = int(blockDim.x), tid = int(threadIdx.x);
+  int* bucket_row = buckets + int64_t(bh) * nkeys;
+  int* cnt = nkeys <= lds_keys ? hist : bucket_row;
+  for (int64_t k = tid; k < nkeys; k += T) cnt[k] = 0;
+  if (bh == 0 && bg.sub_log2 > 0 && queue_fits(p, bg, nkeys))
+    for (int i = tid; i < kQueueInts; i += T) buckets[int64_t(p.B) * p.H * nkeys + i] = 0;
+  __syncthreads();
+
+  const int LP = p.L * p.P;
+  const int64_t ngroups = int64_t(p.Q) * LP / 4;
+  const uint32_t gpq = uint32_t(LP / 4);
+  const char* loc_bh = reinterpret_cast<const char*>(p.loc) + (int64_t(b) * p.Q * p.H + h) * LP * 2 * int64_t(sizeof(TL));
+  const uint32_t loc_q = uint32_t(p.H * LP * 2) * uint32_t(sizeof(TL));
+  auto keys_of = [&](int64_t g, int (&k)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = -1;
+    if (g >= ngroups) return;
+    const uint32_t q = fdiv(uint32_t(g), bg.div_gpq), r = uint32_t(g) - q * gpq;
+    const int l = int(fdiv(r, bg.div_gpl));
+    group_keys<TL>(loc_bh + (q * loc_q + r * uint32_t(8 * sizeof(TL))), levels[l], lt[l], k);
+  };
+  const int64_t step = int64_t(T) * kSmallSortBatch;
+  for (int64_t g0 = tid; g0 < ngroups; g0 += step) {
+    int key[kSmallSortBatch][4];
+#pragma unroll
+    for (int i = 0; i < kSmallSortBatch; ++i) keys_of(g0 + int64_t(i) * T, key[i]);
+#pragma unroll
+    for (int i = 0; i < kSmallSortBatch; ++i)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (key[i][c] >= 0) atomicAdd(&cnt[key[i][c]], 1);
+  }
+  __syncthreads();
+  // Counts to exclusive offsets (the place cursors); the bucket ends go to the row.
+  // Counters in the row were added to at L2; they are read back from there.
+  const bool in_lds = cnt != bucket_row;
+  int carry = 0;
+  for (int64_t k0 = 0; k0 < nkeys; k0 += T) {
+    const int64_t k = k0 + tid;
+    int v = 0;
+    if (k < nkeys) v = in_lds ? cnt[k] : __hip_atomic_load(&cnt[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int sum;
+    const int ex = block_exclusive_scan(v, scan_sums, &sum);
+    if (k < nkeys) {
+      cnt[k] = carry + ex;
+      if (in_lds) bucket_row[k] = carry + ex + v;
+    }
+    carry += sum;
+  }
+  __syncthreads();
+  uint32_t* out = entries + int64_t(bh) * bg.region;
+  for (int64_t g0 = tid; g0 < ngroups; g0 += step) {
+    int key[kSmallSortBatch][4];
+#pragma unroll
+    for (int i = 0; i < kSmallSortBatch; ++i) keys_of(g0 + int64_t(i) * T, key[i]);
+#pragma unroll
+    for (int i = 0; i < kSmallSortBatch; ++i) {
+      int slot[4];
+      group_slots(key[i], cnt, slot);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (key[i][c] >= 0) out[slot[c]] = uint32_t(4 * (g0 + int64_t(i) * T) + c);
     }
   }
 }
@@ -3150,6 +3251,9 @@ struct BackwardPlan {
   int64_t mfma_blocks;
   size_t mfma_lds;
   int mfma_table;         // entries of its queue's prefix table
+  bool small_sort;        // the bucket sort in one launch (msda_bucket_small_kernel)
+  int small_sort_keys;    // its LDS counters
+  size_t small_sort_lds;
   Plan sample;
 };
 
@@ -3218,7 +3322,7 @@ size_t owner_lds_bytes(int dtype, int64_t L, int64_t D, int nb, int cap) {
 int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, int64_t Q, int64_t L,
                        int64_t P, int loc_dtype, const void* const* vec_ptrs, int n_vec,
                        const void* grad_attn, size_t lds_limit, int cus, BackwardPlan* plan,
-                       bool accumulate = false, int paths = 0) {
+                       bool accumulate = false, int paths = 0, int64_t scratch_bytes = -1) {
   // vec_ptrs: value, grad_output, grad_value (channel vectors), then the locations.
   const int n_chan = std::min(n_vec, 3);
   int rc = make_plan(dtype, B, S, H, D, Q, L, P, true, vec_ptrs, n_chan, &plan->sample, elem_size(loc_dtype));
@@ -3249,9 +3353,10 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
     return fail(MSDA_ERR_UNSUPPORTED, "msda: %lld levels do not fit the backward's LDS budget", (long long)L);
   const int64_t samples_bh = Q * L * P;
   bg.region = samples_bh;
-  const int64_t attn_bytes = B * samples_bh * H * es;
+  // The sort's scratch: grad_attention_weights, or the counters region of a workspace.
+  const int64_t attn_bytes = scratch_bytes >= 0 ? scratch_bytes : B * samples_bh * H * es;
   const bool attn_ok = (reinterpret_cast<uintptr_t>(grad_attn) & 3) == 0;
-  bg.keys_alloc = attn_ok && samples_bh < (int64_t(1) << 32) ? attn_bytes / (4 * B * H) : 0;
+  bg.keys_alloc = attn_ok && samples_bh < (int64_t(1) << 32) && B * H > 0 ? attn_bytes / (4 * B * H) : 0;
   // The matrix-core grad_value: float and 16-bit dtypes, D in {16, 32, 48, 64} with
   // 16-byte aligned rows, and its bucket and queue counters (4 per 8 x 8 tile) in the
   // scratch. A level of h x w positions has ceil(h / 8) ceil(w / 8) <= h w / 8 + 1
@@ -3352,6 +3457,19 @@ int make_backward_plan(int dtype, int64_t B, int64_t S, int64_t H, int64_t D, in
   if (bg.chunks > 0)  // a grid-stride loop over (b, h, bucket) when chunked
     plan->scan_blocks = std::max<int64_t>(plan->scan_blocks, std::min<int64_t>((B * H * plan->zero_keys + 255) / 256, 512));
   if (bg.group4) {
+    bg.div_gpq = make_fastdiv(uint32_t(L * P / 4));
+    bg.div_gpl = make_fastdiv(uint32_t(P / 4));
+  }
+  // Small calls: the whole sort in one launch, one workgroup per (b, h), its counters
+  // in LDS (as many as the LDS budget holds; the kernel counts in its scratch row
+  // otherwise).
+  plan->small_sort = plan->bucket && samples_bh <= kSmallSortSamples && (L * P) % 4 == 0 && P % 4 == 0 &&
+                     (loc_ptr == nullptr || aligned(loc_ptr, 16)) && !(paths & MSDA_PATH_ATOMIC_SORT);
+  plan->small_sort_keys = int(std::max<int64_t>(
+      0, std::min<int64_t>(plan->zero_keys, int64_t(budget - std::min(budget, bucket_head + 1024)) / 4)));
+  plan->small_sort_lds = bucket_head + size_t(plan->small_sort_keys) * 4;
+  if (plan->small_sort) {
+    bg.chunks = 0;
     bg.div_gpq = make_fastdiv(uint32_t(L * P / 4));
     bg.div_gpl = make_fastdiv(uint32_t(P / 4));
   }
@@ -3465,6 +3583,14 @@ hipError_t launch_bucket_passes(const BackwardPlan& plan, const Problem& p, int*
 template <typename TL>
 hipError_t launch_buckets(const BackwardPlan& plan, const Problem& p, int* buckets, uint32_t* entries,
                           hipStream_t st) {
+  if (plan.small_sort) {
+    auto k = msda_bucket_small_kernel<TL>;
+    const hipError_t e = allow_lds(k, plan.small_sort_lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, dim3(unsigned(int64_t(p.B) * p.H)), dim3(kSmallSortThreads), plan.small_sort_lds, st, p,
+                       plan.bg, buckets, entries, plan.small_sort_keys);
+    return hipGetLastError();
+  }
   {
     const int64_t n = int64_t(p.B) * p.H * plan.zero_keys;
     const unsigned blocks = unsigned(std::max<int64_t>(1, std::min<int64_t>((n + 255) / 256, 1024)));
@@ -3547,26 +3673,29 @@ Problem make_problem(const void* value, const void* shapes, const void* starts, 
   return p;
 }
 
-// The backward's workspace: the bucket counters, count rows and softmax statistics
-// (as many bytes as grad_attention_weights, the capacity they have there), then one
-// uint32 sample index per sample. Regions 256-byte aligned.
+// The backward's workspace: one uint32 sample index per sample, then the sort's
+// counters, count rows and softmax statistics in the rest (at least as many bytes as
+// grad_attention_weights, the capacity they have there). msda_backward_workspace_size
+// adds room for the bucket and queue counters of the largest tile count the host
+// cannot rule out, so that the matrix-core owners never need the VALU kernel's
+// standby launch (4 x 4 tiles on small levels included; at most a few MB).
 struct WorkspaceLayout {
-  int64_t entries_off, total;
+  int64_t counters_off, base, total;
 };
 
-WorkspaceLayout workspace_layout(int dtype, int64_t B, int64_t H, int64_t Q, int64_t L, int64_t P) {
+WorkspaceLayout workspace_layout(int dtype, int64_t B, int64_t S, int64_t H, int64_t Q, int64_t L, int64_t P) {
   auto align = [](int64_t v) { return (v + 255) / 256 * 256; };
   const int64_t samples = B * Q * H * L * P;
+  const int64_t small_level_tiles = 4 * (kSmallTileTasks / std::max<int64_t>(1, B * H) + 1);
+  const int64_t tiles_bound = L * std::max<int64_t>(S / 8 + 1, small_level_tiles);
+  const int64_t counters = B * H * (4 * tiles_bound + kQueueInts) * 4;
   WorkspaceLayout w;
-  w.entries_off = align(samples * elem_size(dtype));
-  w.total = w.entries_off + align(samples * 4);
+  w.counters_off = align(samples * 4);
+  w.base = w.counters_off + align(samples * elem_size(dtype));
+  w.total = w.counters_off + align(std::max(samples * elem_size(dtype), counters));
   return w;
 }
 
-// The calling thread's side stream on the current device, and its fork and join
-// events (created on first use and kept: a stream of default priority, events
-// without timing). Per thread, so that a capture on one thread never meets another
-// thread's work.
 // Calls of fewer samples keep one stream: there the fork and join cost about as much
 // as the overlap saves (MI355X: 2.6 us more at 129 K samples, even at 154 K, 5 us
 // less at 1 M, 12-19 us less at 4.6-8.3 M).
@@ -3795,15 +3924,17 @@ static int backward_call(const void* value, int value_dtype, const void* spatial
   // The sort's scratch: the caller's workspace when it is large enough (then
   // grad_sample may run beside the sort), else grad_attention_weights and
   // grad_sampling_locations (then grad_sample runs last).
-  const WorkspaceLayout wl = workspace_layout(value_dtype, batch, heads, queries, levels, points);
-  const bool use_ws = workspace != nullptr && workspace_bytes >= wl.total && aligned(workspace, 256);
+  const WorkspaceLayout wl = workspace_layout(value_dtype, batch, spatial, heads, queries, levels, points);
+  const bool use_ws = workspace != nullptr && workspace_bytes >= wl.base && aligned(workspace, 256);
+  void* counters = use_ws ? static_cast<char*>(workspace) + wl.counters_off : grad_attention_weights;
   BackwardPlan plan;
   size_t lds_limit;
   int cus;
   device_info(&lds_limit, &cus);
   rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
-                          loc_dtype, vec, 4, use_ws ? workspace : grad_attention_weights, lds_limit, cus, &plan,
-                          accumulate, g_path_override.load(std::memory_order_relaxed));
+                          loc_dtype, vec, 4, counters, lds_limit, cus, &plan, accumulate,
+                          g_path_override.load(std::memory_order_relaxed),
+                          use_ws ? workspace_bytes - wl.counters_off : -1);
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,
@@ -3827,9 +3958,8 @@ static int backward_call(const void* value, int value_dtype, const void* spatial
   // Scratch of the bucket sort: counters in grad_attention_weights, sample indices in
   // grad_sampling_locations, which msda_grad_sample_kernel overwrites last; or the
   // workspace.
-  int* buckets = static_cast<int*>(use_ws ? workspace : grad_attention_weights);
-  uint32_t* entries = use_ws ? reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + wl.entries_off)
-                             : static_cast<uint32_t*>(grad_sampling_locations);
+  int* buckets = static_cast<int*>(counters);
+  uint32_t* entries = use_ws ? static_cast<uint32_t*>(workspace) : static_cast<uint32_t*>(grad_sampling_locations);
   // grad_sample beside the sort: it needs neither the sort nor grad_value, and with
   // the scratch in the workspace it writes nothing the sort uses. Only where it adds
   // nothing into grad_value (the matrix-core owners take every level, overlapping ones
@@ -3920,10 +4050,9 @@ int msda_backward_workspace_size(int value_dtype, int64_t batch, int64_t spatial
     return fail(MSDA_ERR_INVALID, "msda: unknown value dtype code %d", value_dtype);
   if (batch < 0 || spatial < 0 || heads < 0 || channels < 0 || queries < 0 || levels < 0 || points < 0)
     return fail(MSDA_ERR_INVALID, "msda: negative size");
-  (void)spatial;
   (void)channels;
   (void)flags;
-  *bytes = workspace_layout(value_dtype, batch, heads, queries, levels, points).total;
+  *bytes = workspace_layout(value_dtype, batch, spatial, heads, queries, levels, points).total;
   return MSDA_OK;
 }
 
@@ -3952,7 +4081,7 @@ int msda_backward_no_alloc(const void* value, int value_dtype, const void* spati
                       queries, levels, points, flags,
                       MSDA_SOFTMAX | MSDA_ACCUMULATE_GRAD_VALUE | MSDA_GRAD_VALUE_ATOMIC);
   if (rc != MSDA_OK) return rc;
-  const int64_t need = workspace_layout(value_dtype, batch, heads, queries, levels, points).total;
+  const int64_t need = workspace_layout(value_dtype, batch, spatial, heads, queries, levels, points).base;
   if (need > kScratchBytes)
     return fail(MSDA_ERR_INVALID,
                 "msda_backward_no_alloc: these sizes need %lld bytes of scratch, the static scratch holds %lld "

@@ -162,11 +162,16 @@ int msda_backward(const void* value, int value_dtype,
  * and MSDA_GRAD_VALUE_ATOMIC is off) and the call has at least 2^19 samples, the call
  * forks it onto a side stream of the calling thread (created on the first such call
  * per thread and device, default priority) beside the sort, and joins the caller's
- * stream before the grad_value kernel (12 us less at B = 4, Q = 21,504 in bf16). Work before the call on `stream` happens before all of it, and work after
- * the call after all of it, so it stays stream-ordered and can be captured in a HIP
- * graph. The workspace is as large as grad_attention_weights plus 4 bytes per sample
- * (49.5 MB at B = 4, Q = 21,504, H = 8, L = 3, P = 4 in bf16). With a null or smaller
- * workspace the call is msda_backward.
+ * stream before the grad_value kernel (12 us less at B = 4, Q = 21,504 in bf16).
+ * Work before the call on `stream` happens before all of it, and work after the call
+ * after all of it, so it stays stream-ordered and can be captured in a HIP graph.
+ * The workspace holds 4 bytes per sample, then at least as many bytes as
+ * grad_attention_weights, and room for the bucket counters of the largest tile count
+ * the sizes allow, so that the grad_value kernel never needs its fallback launch
+ * (49.5 MB at B = 4, Q = 21,504, H = 8, L = 3, P = 4 in bf16; 5.2 MB for 300 queries
+ * on a 17,821-position pyramid in float32). A smaller workspace that still holds the
+ * indices and grad_attention_weights' bytes works too, with that fallback where it
+ * is needed; a null or yet smaller one makes the call msda_backward.
  *
  * Replaces the same backward operator as msda_backward.
  */

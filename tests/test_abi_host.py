@@ -97,16 +97,25 @@ def workspace_call(lib, *, vdt=2, sizes=(4, 21504, 8, 32, 21504, 3, 4), flags=0,
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
-@pytest.mark.parametrize("sizes", [(4, 21504, 8, 32, 21504, 3, 4), (1, 100, 3, 5, 7, 2, 3), (2, 10, 1, 4, 0, 1, 1)])
-def test_workspace_size_is_the_weight_gradient_and_one_index_per_sample(lib, dtype, sizes):
+@pytest.mark.parametrize("sizes", [(4, 21504, 8, 32, 21504, 3, 4), (4, 17821, 8, 32, 300, 4, 4),
+                                   (1, 100, 3, 5, 7, 2, 3), (2, 10, 1, 4, 0, 1, 1)])
+def test_workspace_size_holds_the_indices_and_the_counters(lib, dtype, sizes):
+    """One uint32 index per sample, then a counters region at least as large as the
+    weight gradient (the capacity the plain call has) and as the bucket and queue
+    counters of the largest tile count the host cannot rule out: L (S / 8 + 1) tiles of
+    8 x 8 (a one-row level), or the 4 x 4 tiles of small levels, 4 counters each, plus
+    288 queue ints, per (b, h)."""
     from deformops_amd.backends.hip import _bridge  # noqa: PLC0415
 
     B, S, H, D, Q, L, P = sizes  # noqa: N806
     samples = B * Q * H * L * P
     size = lib.workspace_size(dtype, *sizes)
-    assert size == _bridge._workspace_bytes(lib, dtype, B, Q, H, L, P)  # noqa: SLF001
+    assert size == _bridge._workspace_bytes(dtype, B, S, H, Q, L, P)  # noqa: SLF001
     assert size % 256 == 0
-    assert samples * (dtype.itemsize + 4) <= size < samples * (dtype.itemsize + 4) + 512
+    align = lambda v: (v + 255) // 256 * 256  # noqa: E731
+    tiles = L * max(S // 8 + 1, 4 * (384 // max(1, B * H) + 1))
+    counters = B * H * (4 * tiles + 9 * 32) * 4
+    assert size == align(samples * 4) + align(max(samples * dtype.itemsize, counters))
     if sizes == (4, 21504, 8, 32, 21504, 3, 4) and dtype == torch.bfloat16:
         assert size == 49_545_216  # the size the header quotes
 

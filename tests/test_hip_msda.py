@@ -499,6 +499,19 @@ def test_workspace_backward_matches_the_plain_backward(device, cfg, dtype, batch
         torch.testing.assert_close(got[2], plain[2], rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("dtype", [BF16, F32], ids=["bf16", "f32"])
+def test_small_sort_counts_in_its_scratch_row_when_lds_is_short(device, dtype):
+    """A call of few samples per (b, h) sorts in one launch, its bucket counters in
+    LDS. A 1024 x 1024 level has 16,384 tiles of 8 x 8, 65,536 counters, more than
+    the 160 KB of LDS hold, so the kernel counts in its own row of the workspace's
+    scratch instead (the autograd bridge passes a workspace that holds them)."""
+    w = make_workload(1, batch=1, queries=60, heads=2, channels=16, levels=((1024, 1024),), locations="uniform")
+    w = w.to(device, dtype)
+    for softmax in (False, True):
+        check_against_oracle(*w.operands(softmax=softmax), w.grad_output, softmax=softmax, dtype=dtype,
+                             label="one 1024 x 1024 level")
+
+
 @pytest.mark.parametrize("entry", ["plain", "workspace"])
 @pytest.mark.parametrize("dtype", [BF16, F32], ids=["bf16", "f32"])
 def test_calls_replay_from_a_hip_graph(device, dtype, entry):
