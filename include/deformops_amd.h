@@ -231,12 +231,14 @@ int msda_abi_version(void);
  * up to rounding. Not meant to be changed while calls run on other threads. */
 int msda_set_path_override(int paths);
 
-/* Makes later msda_backward calls on the calling thread record the four HIP events
- * events[0..3] (hipEvent_t, created by the caller) on their stream: before the
- * bucket sort, after the sort (and the softmax statistics), after grad_value, and
- * after grad_sample; count 0 stops it. No counterpart in the reference: a
- * measurement hook, so that a benchmark can time each phase of a backward call
- * (bench.py rates each kernel by its L2 requests per second). */
+/* Makes later backward calls (any of the three entry points) on the calling thread
+ * record the four HIP events events[0..3] (hipEvent_t, created by the caller) on
+ * their stream: before the bucket sort, after the sort (and the softmax
+ * statistics), after grad_value, and after grad_sample; count 0 stops it. While the
+ * events are set the kernels run in that order on the caller's stream (no side
+ * stream). No counterpart in the reference: a measurement hook, so that a benchmark
+ * can time each phase of a backward call (bench.py rates each kernel by its L2
+ * requests per second). */
 int msda_set_phase_events(void* const* events, int count);
 
 /* The launch layout msda_forward / msda_backward would use for these sizes:
