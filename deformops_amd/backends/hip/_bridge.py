@@ -134,7 +134,7 @@ def _launch_backward(value: Tensor, shapes: Tensor, starts: Tensor, loc: Tensor,
     lib = _lib.load()
     # The sort's scratch in a workspace of its own (the caching allocator's blocks are
     # 512-byte aligned), so that the location and weight gradients need not wait for it.
-    workspace = torch.empty(_workspace_bytes(value.dtype, B, S, H, Q, L, P), dtype=torch.uint8,
+    workspace = torch.empty(_workspace_bytes(value.dtype, B, S, H, Q, L, P, softmax), dtype=torch.uint8,
                             device=value.device)
     with _on_device(value.device):
         status = lib.backward_workspace(
@@ -153,9 +153,10 @@ def _launch_backward(value: Tensor, shapes: Tensor, starts: Tensor, loc: Tensor,
 
 
 @functools.lru_cache(maxsize=256)
-def _workspace_bytes(dtype: torch.dtype, B: int, S: int, H: int, Q: int, L: int, P: int) -> int:  # noqa: N803
+def _workspace_bytes(dtype: torch.dtype, B: int, S: int, H: int, Q: int, L: int, P: int,  # noqa: N803
+                     softmax: bool) -> int:
     """msda_backward_workspace_size for these sizes, asked of the library once per shape."""
-    return _lib.load().workspace_size(dtype, B, S, H, 0, Q, L, P)
+    return _lib.load().workspace_size(dtype, B, S, H, 0, Q, L, P, _lib.FLAG_SOFTMAX if softmax else 0)
 
 
 def _normalized(value: Tensor, spatial_shapes: Tensor, level_start_index: Tensor, loc: Tensor,

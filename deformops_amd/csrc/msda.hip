@@ -372,6 +372,10 @@ struct Problem {
   int sort_overlap;
   int zero_gv;  // grad_value starts at zero (not accumulated into)
   int es;       // bytes of one value element
+  // Softmax backward with grad_sample beside the sort: grad_sample writes every
+  // unit's log-sum-exp here (a SoftStat per (b, q, h)) for the grad_value kernel, in
+  // place of msda_softmax_stats_kernel. Null otherwise.
+  char* stats;
 };
 
 // One pyramid level as the kernels use it. A level whose table entry does not fit
@@ -619,7 +623,8 @@ template <typename T, typename TL, bool SOFTMAX>
 __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const Level* levels,
                                      const UnitRaw& raw, Staged<typename Elem<T>::acc>* wst,
                                      typename Elem<T>::acc& smax,
-                                     typename Elem<T>::acc& sinv) {
+                                     typename Elem<T>::acc& sinv,
+                                     typename Elem<T>::acc* ssum = nullptr) {
   using A = typename Elem<T>::acc;
   constexpr int ES = Elem<T>::size;
   const int LP = p.L * p.P;
@@ -638,6 +643,7 @@ __device__ inline void stage_samples(const Problem& p, const LaneMap& m, const L
     sum = unit_sum(sum, m.lh);
     smax = mx;
     sinv = A(1) / sum;
+    if (ssum) *ssum = sum;
   }
   if (!m.unit_ok) return;
   for (int s = m.t; s < LP; s += m.lh) {
@@ -1807,7 +1813,9 @@ __global__ __launch_bounds__(kOwnerThreads) void msda_grad_value_kernel(
   if (ntiles <= 0) return;
   if (after_mfma && queue_fits(p, bg, 4 * ntiles)) return;  // the matrix-core kernel did the work
   const bool bucketed = 4 * ntiles <= bg.keys_alloc;
-  const SoftStat<A>* stats = SOFTMAX && bucketed && softmax_stats_fit<A>(p, bg, 4 * ntiles, buckets)
+  const SoftStat<A>* stats = !SOFTMAX ? nullptr
+                             : p.stats ? reinterpret_cast<const SoftStat<A>*>(p.stats)
+                             : bucketed && softmax_stats_fit<A>(p, bg, 4 * ntiles, buckets)
                                  ? softmax_stats<A>(const_cast<int*>(buckets), p, 4 * ntiles)
                                  : nullptr;
   if (tid == 0) {
@@ -2664,7 +2672,7 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
     }
   }
   if (ntiles <= 0 || !queue_fits(p, bg, 4 * ntiles)) return;  // the VALU owner kernel runs instead
-  const bool stats_ok = SOFTMAX && softmax_stats_fit<float>(p, bg, 4 * ntiles, buckets);
+  const bool stats_ok = SOFTMAX && (p.stats || softmax_stats_fit<float>(p, bg, 4 * ntiles, buckets));
   if (tid == 0) {
     order_levels(p, levels, lt, order, rank_base);
     // R x R regions, R the power of two nearest the finest level's tile count, at most
@@ -2851,7 +2859,9 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
       t.div_lp = bg.div_lp;
       t.LP = LP;
       t.H = p.H;
-      t.stats = SOFTMAX && stats_ok ? softmax_stats<float>(buckets, p, 4 * ntiles) + unit0 : nullptr;
+      t.stats = SOFTMAX && stats_ok ? (p.stats ? reinterpret_cast<const SoftStat<float>*>(p.stats)
+                                               : softmax_stats<float>(buckets, p, 4 * ntiles)) + unit0
+                                    : nullptr;
 
       f32x4_v acc[4][NB];
       // All K-blocks (per-wave mode), or K-blocks wave, wave + 4, ...
@@ -2994,8 +3004,10 @@ __global__ __launch_bounds__(kWave * kMaxWavesPerBlock) void msda_grad_sample_ke
   load_levels(p, levels);
   __syncthreads();
   overlap_flag_raise(levels, p.L);
-  A smax, sinv;
-  stage_samples<T, TL, SOFTMAX>(p, m, levels, raw, wst, smax, sinv);
+  A smax, sinv, ssum = A(1);
+  stage_samples<T, TL, SOFTMAX>(p, m, levels, raw, wst, smax, sinv, &ssum);
+  if constexpr (SOFTMAX)  // the unit's log-sum-exp for the grad_value kernel, as msda_softmax_stats_kernel's
+    if (p.stats && m.unit_ok && m.t == 0) reinterpret_cast<SoftStat<A>*>(p.stats)[m.gunit] = SoftStat<A>{smax + log(ssum)};
   __syncthreads();
   // grad_value by atomics: asked for, or levels overlap where the owners stand aside
   // (the sort and the owners then only zeroed grad_value).
@@ -3678,21 +3690,27 @@ Problem make_problem(const void* value, const void* shapes, const void* starts, 
 // grad_attention_weights, the capacity they have there). msda_backward_workspace_size
 // adds room for the bucket and queue counters of the largest tile count the host
 // cannot rule out, so that the matrix-core owners never need the VALU kernel's
-// standby launch (4 x 4 tiles on small levels included; at most a few MB).
+// standby launch (4 x 4 tiles on small levels included; at most a few MB), and, for
+// the softmax method, a region of its own for the per-unit softmax statistics, which
+// grad_sample then writes on its side stream.
 struct WorkspaceLayout {
-  int64_t counters_off, base, total;
+  int64_t counters_off, counters_bytes, stats_off, base, total;
 };
 
-WorkspaceLayout workspace_layout(int dtype, int64_t B, int64_t S, int64_t H, int64_t Q, int64_t L, int64_t P) {
+WorkspaceLayout workspace_layout(int dtype, int64_t B, int64_t S, int64_t H, int64_t Q, int64_t L, int64_t P,
+                                 bool softmax) {
   auto align = [](int64_t v) { return (v + 255) / 256 * 256; };
   const int64_t samples = B * Q * H * L * P;
   const int64_t small_level_tiles = 4 * (kSmallTileTasks / std::max<int64_t>(1, B * H) + 1);
   const int64_t tiles_bound = L * std::max<int64_t>(S / 8 + 1, small_level_tiles);
   const int64_t counters = B * H * (4 * tiles_bound + kQueueInts) * 4;
+  const int64_t stat_bytes = dtype == MSDA_F64 ? 8 : 4;  // SoftStat of the accumulation type
   WorkspaceLayout w;
   w.counters_off = align(samples * 4);
+  w.counters_bytes = align(std::max(samples * elem_size(dtype), counters));
   w.base = w.counters_off + align(samples * elem_size(dtype));
-  w.total = w.counters_off + align(std::max(samples * elem_size(dtype), counters));
+  w.stats_off = w.counters_off + w.counters_bytes;
+  w.total = w.stats_off + (softmax ? align(B * Q * H * stat_bytes) : 0);
   return w;
 }
 
@@ -3924,8 +3942,11 @@ static int backward_call(const void* value, int value_dtype, const void* spatial
   // The sort's scratch: the caller's workspace when it is large enough (then
   // grad_sample may run beside the sort), else grad_attention_weights and
   // grad_sampling_locations (then grad_sample runs last).
-  const WorkspaceLayout wl = workspace_layout(value_dtype, batch, spatial, heads, queries, levels, points);
+  const bool softmax = flags & MSDA_SOFTMAX;
+  const WorkspaceLayout wl = workspace_layout(value_dtype, batch, spatial, heads, queries, levels, points, softmax);
   const bool use_ws = workspace != nullptr && workspace_bytes >= wl.base && aligned(workspace, 256);
+  // A workspace of the full size gives the softmax statistics a region of their own.
+  const bool ws_stats = use_ws && softmax && workspace_bytes >= wl.total;
   void* counters = use_ws ? static_cast<char*>(workspace) + wl.counters_off : grad_attention_weights;
   BackwardPlan plan;
   size_t lds_limit;
@@ -3934,7 +3955,7 @@ static int backward_call(const void* value, int value_dtype, const void* spatial
   rc = make_backward_plan(value_dtype, batch, spatial, heads, channels, queries, levels, points,
                           loc_dtype, vec, 4, counters, lds_limit, cus, &plan, accumulate,
                           g_path_override.load(std::memory_order_relaxed),
-                          use_ws ? workspace_bytes - wl.counters_off : -1);
+                          !use_ws ? -1 : ws_stats ? wl.counters_bytes : workspace_bytes - wl.counters_off);
   if (rc != MSDA_OK) return rc;
   Problem p = make_problem(value, spatial_shapes, level_start_index, index_dtype,
                            sampling_locations, attention_weights, batch, spatial, heads,
@@ -3968,8 +3989,10 @@ static int backward_call(const void* value, int value_dtype, const void* spatial
   if (fork && use_ws && p.sort_overlap && sample_count >= kSideStreamSamples && !g_phase_events_on) {
     side = side_stream();
     if (side == nullptr) return fail(MSDA_ERR_HIP, "msda_backward_workspace: no side stream: %s", hipGetErrorString(hipGetLastError()));
+    // grad_sample, which forms each unit's softmax anyway, leaves the statistics for
+    // the grad_value kernel in the workspace: no statistics pass after the sort.
+    if (ws_stats) p.stats = static_cast<char*>(workspace) + wl.stats_off;
   }
-  const bool softmax = flags & MSDA_SOFTMAX;
   const hipError_t err = dispatch(
       value_dtype, loc_dtype == MSDA_F32 && value_dtype != MSDA_F32, plan.sample.cv,
       [&]<typename T, typename TL, int CV>() {
@@ -3986,7 +4009,7 @@ static int backward_call(const void* value, int value_dtype, const void* spatial
         if (plan.bucket && !atomic_gv) {
           e = launch_buckets<TL>(plan, p, buckets, entries, st);
           if (e != hipSuccess) return e;
-          if (softmax) {  // per-unit softmax statistics, where the scratch has room
+          if (softmax && !p.stats) {  // per-unit softmax statistics, where the scratch has room
             const int64_t units = int64_t(p.B) * p.Q * p.H;
             const unsigned blocks = unsigned(std::max<int64_t>(1, std::min<int64_t>((units + 255) / 256, 2048)));
             const size_t lds = p.L > kMaxOrderedLevels ? (sizeof(Level) + sizeof(LevelTiles)) * size_t(p.L) : 0;
@@ -4004,13 +4027,16 @@ static int backward_call(const void* value, int value_dtype, const void* spatial
           e = hipGetLastError();
           if (e != hipSuccess) return e;
         }
-        if (plan.mfma && !atomic_gv)
-          e = softmax ? launch_owner_mfma<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
-                      : launch_owner_mfma<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
-        if (side) {  // grad_sample done before the owners (whose LDS would keep it from overlapping)
+        // The join: before the grad_value kernel when it reads the softmax statistics
+        // grad_sample leaves; otherwise after it, so that grad_sample's tail overlaps it.
+        if (side && p.stats) {
           e = hipStreamWaitEvent(st, side->join, 0);
           if (e != hipSuccess) return e;
         }
+        if (plan.mfma && !atomic_gv)
+          e = softmax ? launch_owner_mfma<T, TL, true>(plan, p, buckets, entries, int(accumulate), st)
+                      : launch_owner_mfma<T, TL, false>(plan, p, buckets, entries, int(accumulate), st);
+        if (e == hipSuccess && side && !p.stats) e = hipStreamWaitEvent(st, side->join, 0);
         if (e == hipSuccess && !atomic_gv && (!plan.mfma || plan.mfma_fallback)) {
           const int after_mfma = plan.mfma ? 1 : 0;
           e = softmax ? launch_owner_cvr<T, TL, true>(plan, p, buckets, entries, int(accumulate), after_mfma, st)
@@ -4051,8 +4077,7 @@ int msda_backward_workspace_size(int value_dtype, int64_t batch, int64_t spatial
   if (batch < 0 || spatial < 0 || heads < 0 || channels < 0 || queries < 0 || levels < 0 || points < 0)
     return fail(MSDA_ERR_INVALID, "msda: negative size");
   (void)channels;
-  (void)flags;
-  *bytes = workspace_layout(value_dtype, batch, spatial, heads, queries, levels, points).total;
+  *bytes = workspace_layout(value_dtype, batch, spatial, heads, queries, levels, points, flags & MSDA_SOFTMAX).total;
   return MSDA_OK;
 }
 
@@ -4081,7 +4106,7 @@ int msda_backward_no_alloc(const void* value, int value_dtype, const void* spati
                       queries, levels, points, flags,
                       MSDA_SOFTMAX | MSDA_ACCUMULATE_GRAD_VALUE | MSDA_GRAD_VALUE_ATOMIC);
   if (rc != MSDA_OK) return rc;
-  const int64_t need = workspace_layout(value_dtype, batch, spatial, heads, queries, levels, points).base;
+  const int64_t need = workspace_layout(value_dtype, batch, spatial, heads, queries, levels, points, false).base;
   if (need > kScratchBytes)
     return fail(MSDA_ERR_INVALID,
                 "msda_backward_no_alloc: these sizes need %lld bytes of scratch, the static scratch holds %lld "

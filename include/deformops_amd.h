@@ -161,17 +161,22 @@ int msda_backward(const void* value, int value_dtype,
  * grad_value (the matrix-core owners take every level, overlapping ones included,
  * and MSDA_GRAD_VALUE_ATOMIC is off) and the call has at least 2^19 samples, the call
  * forks it onto a side stream of the calling thread (created on the first such call
- * per thread and device, default priority) beside the sort, and joins the caller's
- * stream before the grad_value kernel (12 us less at B = 4, Q = 21,504 in bf16).
+ * per thread and device, default priority) beside the sort and the grad_value
+ * kernel, and joins the caller's stream at the end of the call (with MSDA_SOFTMAX,
+ * before the grad_value kernel, which then reads the softmax statistics grad_sample
+ * leaves): 9-13 us less at B = 4, Q = 21,504 in bf16, 21 us with softmax.
  * Work before the call on `stream` happens before all of it, and work after the call
  * after all of it, so it stays stream-ordered and can be captured in a HIP graph.
  * The workspace holds 4 bytes per sample, then at least as many bytes as
  * grad_attention_weights, and room for the bucket counters of the largest tile count
  * the sizes allow, so that the grad_value kernel never needs its fallback launch
  * (49.5 MB at B = 4, Q = 21,504, H = 8, L = 3, P = 4 in bf16; 5.2 MB for 300 queries
- * on a 17,821-position pyramid in float32). A smaller workspace that still holds the
- * indices and grad_attention_weights' bytes works too, with that fallback where it
- * is needed; a null or yet smaller one makes the call msda_backward.
+ * on a 17,821-position pyramid in float32). With MSDA_SOFTMAX it also holds one
+ * softmax statistic per (b, q, h) (4 bytes, 8 in float64: 2.75 MB more at that
+ * workload), which the forked grad_sample writes, so that no statistics pass follows
+ * the sort. A smaller workspace that still holds the indices and
+ * grad_attention_weights' bytes works too, with that fallback and that pass where
+ * they are needed; a null or yet smaller one makes the call msda_backward.
  *
  * Replaces the same backward operator as msda_backward.
  */
@@ -187,8 +192,9 @@ int msda_backward_workspace(const void* value, int value_dtype,
                             int64_t queries, int64_t levels, int64_t points,
                             int flags, void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Bytes of workspace msda_backward_workspace takes for these sizes. Host only. No
- * counterpart in the reference (its scratch is allocated inside the op). */
+/* Bytes of workspace msda_backward_workspace takes for these sizes and flags (only
+ * MSDA_SOFTMAX changes it). Host only. No counterpart in the reference (its scratch
+ * is allocated inside the op). */
 int msda_backward_workspace_size(int value_dtype, int64_t batch, int64_t spatial, int64_t heads,
                                  int64_t channels, int64_t queries, int64_t levels, int64_t points,
                                  int flags, int64_t* bytes);

@@ -96,27 +96,31 @@ def workspace_call(lib, *, vdt=2, sizes=(4, 21504, 8, 32, 21504, 3, 4), flags=0,
     return lib.backward_workspace(p, vdt, p, p, 0, p, 2, p, p, p, p, p, *sizes, flags, p, ws_bytes, None)
 
 
+@pytest.mark.parametrize("softmax", [False, True], ids=["linear", "softmax"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16, torch.float64])
 @pytest.mark.parametrize("sizes", [(4, 21504, 8, 32, 21504, 3, 4), (4, 17821, 8, 32, 300, 4, 4),
                                    (1, 100, 3, 5, 7, 2, 3), (2, 10, 1, 4, 0, 1, 1)])
-def test_workspace_size_holds_the_indices_and_the_counters(lib, dtype, sizes):
+def test_workspace_size_holds_the_indices_and_the_counters(lib, dtype, sizes, softmax):
     """One uint32 index per sample, then a counters region at least as large as the
     weight gradient (the capacity the plain call has) and as the bucket and queue
     counters of the largest tile count the host cannot rule out: L (S / 8 + 1) tiles of
     8 x 8 (a one-row level), or the 4 x 4 tiles of small levels, 4 counters each, plus
-    288 queue ints, per (b, h)."""
+    288 queue ints, per (b, h); with softmax, then one statistic (float, double for
+    float64) per (b, q, h)."""
     from deformops_amd.backends.hip import _bridge  # noqa: PLC0415
 
     B, S, H, D, Q, L, P = sizes  # noqa: N806
     samples = B * Q * H * L * P
-    size = lib.workspace_size(dtype, *sizes)
-    assert size == _bridge._workspace_bytes(dtype, B, S, H, Q, L, P)  # noqa: SLF001
+    flags = _lib.FLAG_SOFTMAX if softmax else 0
+    size = lib.workspace_size(dtype, *sizes, flags)
+    assert size == _bridge._workspace_bytes(dtype, B, S, H, Q, L, P, softmax)  # noqa: SLF001
     assert size % 256 == 0
     align = lambda v: (v + 255) // 256 * 256  # noqa: E731
     tiles = L * max(S // 8 + 1, 4 * (384 // max(1, B * H) + 1))
     counters = B * H * (4 * tiles + 9 * 32) * 4
-    assert size == align(samples * 4) + align(max(samples * dtype.itemsize, counters))
-    if sizes == (4, 21504, 8, 32, 21504, 3, 4) and dtype == torch.bfloat16:
+    stats = align(B * Q * H * (8 if dtype == torch.float64 else 4)) if softmax else 0
+    assert size == align(samples * 4) + align(max(samples * dtype.itemsize, counters)) + stats
+    if sizes == (4, 21504, 8, 32, 21504, 3, 4) and dtype == torch.bfloat16 and not softmax:
         assert size == 49_545_216  # the size the header quotes
 
 

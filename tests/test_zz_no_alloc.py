@@ -59,7 +59,9 @@ def test_no_alloc_backward_matches_the_workspace_backward(device, dtype, softmax
     # the scratch), then a smaller one on top of what it left there.
     works = [make_workload(4).to(device, dtype), make_workload(2, batch=1, queries=3000, seed=7).to(device, dtype)]
     for i, w in enumerate(works):
-        assert lib.workspace_size(dtype, *w.sizes, flags) <= SCRATCH_BYTES
+        # The scratch holds the indices and the counters (the linear method's workspace);
+        # the softmax statistics' region of the workspace entry is not needed here.
+        assert lib.workspace_size(dtype, *w.sizes, 0) <= SCRATCH_BYTES
         want = [torch.empty_like(t) for t in (w.value, w.sampling_locations, w.attention_weights)]
         got = [torch.full_like(t, float("nan")) for t in want]
         call(lib, "workspace", w, want, flags)
