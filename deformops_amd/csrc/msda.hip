@@ -2712,7 +2712,10 @@ __global__ __launch_bounds__(kWave * kMfmaWaves, mfma_blocks_per_cu(NB, int(size
   const int64_t npairs = int64_t(p.B) * R * R;
   const int64_t pa = xcd * npairs / kXcds, pb = (xcd + 1) * npairs / kXcds;
   const int64_t nentries = (pb - pa) * p.L;
-  const bool regional = nentries <= table_cap;
+  // The same choice on every XCD (the queues' pair counts differ by one when npairs
+  // is not a multiple of 8): either every queue holds (pair, level) entries or every
+  // queue holds an eighth of each level's tasks, never a mix of the two.
+  const bool regional = (npairs + kXcds - 1) / kXcds * p.L <= table_cap;
   int64_t queue_len = 0;
   if (regional) {
     // Chunks per (pair, level), then their exclusive prefix sums: four entries a thread.

@@ -512,6 +512,17 @@ def test_small_sort_counts_in_its_scratch_row_when_lds_is_short(device, dtype):
                              label="one 1024 x 1024 level")
 
 
+def test_many_images_keep_one_queue_mode(device):
+    """The matrix-core grad_value kernel deals (image, region) pairs to eight XCD
+    queues. With 8,193 images of one 8 x 8 level (one region each) the queues get
+    1,024 or 1,025 pairs, around the 1,024 entries a queue's LDS table holds: every
+    queue must then take the same mode (here the raster split of each level's tasks),
+    or tasks would be done twice and others never."""
+    w = make_workload(0, batch=8193, queries=1, heads=1, channels=16, levels=((8, 8),), locations="uniform")
+    w = w.to(device, BF16)
+    check_against_oracle(*w.operands(), w.grad_output, softmax=False, dtype=BF16, label="8193 images")
+
+
 @pytest.mark.parametrize("entry", ["plain", "workspace"])
 @pytest.mark.parametrize("dtype", [BF16, F32], ids=["bf16", "f32"])
 def test_calls_replay_from_a_hip_graph(device, dtype, entry):
