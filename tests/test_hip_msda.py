@@ -517,8 +517,9 @@ def test_many_images_keep_one_queue_mode(device):
     queues. With 8,193 images of one 8 x 8 level (one region each) the queues get
     1,024 or 1,025 pairs, around the 1,024 entries a queue's LDS table holds: every
     queue must then take the same mode (here the raster split of each level's tasks),
-    or tasks would be done twice and others never."""
-    w = make_workload(0, batch=8193, queries=1, heads=1, channels=16, levels=((8, 8),), locations="uniform")
+    or tasks would be done twice and others never (with two heads the two splits
+    differ: image 7,168's first head belonged to neither)."""
+    w = make_workload(0, batch=8193, queries=1, heads=2, channels=16, levels=((8, 8),), locations="uniform")
     w = w.to(device, BF16)
     check_against_oracle(*w.operands(), w.grad_output, softmax=False, dtype=BF16, label="8193 images")
 
