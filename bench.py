@@ -10,8 +10,9 @@ public API (lower is better), timed over exactly ``--steps`` steps after
 ``--warmup`` untimed ones. Before anything is timed the GPU runs the workload's
 C-ABI fwd+bwd pair, untimed, for 0.3 s (``config.untimed_settle``), so that its
 clocks have left the idle state, and before the public-API steps it runs those
-steps, untimed, for another 0.3 s (fresh allocator blocks are slower at first). ``roofline`` rates one fwd+bwd pair of C-ABI calls
-(the forward kernel, then the backward's kernels, back to back on one stream,
+steps, untimed, for another 0.3 s (fresh allocator blocks are slower at first).
+``roofline`` rates one fwd+bwd pair of C-ABI calls (msda_forward, then
+msda_backward_workspace as the autograd bridge calls it, back to back on one stream,
 bracketed by HIP events on that stream) by its algorithmic bytes against 8 TB/s;
 ``roofline.backward_call`` rates the backward call alone, and ``roofline.gather``
 rates the forward kernel's corner gathers against the random-row gather rate of
@@ -502,8 +503,8 @@ def main() -> int:
             # of grad_value's scattered candidate reads: "binding" and "l2_requests".
             "bound": "hbm",
             "binding": "l2_request_rate (forward, grad_sample); memory latency (grad_value)",
-            "kernel": "one msda_forward + msda_backward C-ABI call pair (forward kernel, bucket sort, "
-                      "grad_value, grad_sample), back to back on one stream",
+            "kernel": "one msda_forward + msda_backward_workspace C-ABI call pair (forward kernel, bucket sort, "
+                      "grad_value, grad_sample beside the sort on a side stream), on one caller stream",
             "achieved": round(call_gbs, 1),
             "peak": PEAK_HBM_GBS,
             "unit": "GB/s",
