@@ -3717,10 +3717,13 @@ WorkspaceLayout workspace_layout(int dtype, int64_t B, int64_t S, int64_t H, int
   return w;
 }
 
-// Calls of fewer samples keep one stream: there the fork and join cost about as much
-// as the overlap saves (MI355X: 2.6 us more at 129 K samples, even at 154 K, 5 us
-// less at 1 M, 12-19 us less at 4.6-8.3 M).
-constexpr int64_t kSideStreamSamples = int64_t(1) << 19;
+// Calls of fewer samples keep one stream. The overlap saves GPU time in proportion
+// to the samples (MI355X: 2.6 us more at 129 K samples, 5 us less at 1 M, 10-37 us
+// less at 4.6-8.3 M), but the fork and join cost the calling thread about 45 us
+// (two hipStreamWaitEvent calls of 12-16 us each and a launch on a second queue,
+// against 14 us for the whole one-stream call). Where the backward's GPU time is
+// not well above the host time of a training step, that delay is the step's.
+constexpr int64_t kSideStreamSamples = int64_t(1) << 21;
 
 struct SideStream {
   hipStream_t stream = nullptr;

@@ -159,12 +159,14 @@ int msda_backward(const void* value, int value_dtype,
  * grad_attention_weights and grad_sampling_locations, so the location and weight
  * gradient kernel no longer has to run after it: where that kernel adds nothing into
  * grad_value (the matrix-core owners take every level, overlapping ones included,
- * and MSDA_GRAD_VALUE_ATOMIC is off) and the call has at least 2^19 samples, the call
+ * and MSDA_GRAD_VALUE_ATOMIC is off) and the call has at least 2^21 samples, the call
  * forks it onto a side stream of the calling thread (created on the first such call
  * per thread and device, default priority) beside the sort and the grad_value
  * kernel, and joins the caller's stream at the end of the call (with MSDA_SOFTMAX,
  * before the grad_value kernel, which then reads the softmax statistics grad_sample
- * leaves): 9-13 us less at B = 4, Q = 21,504 in bf16, 21 us with softmax.
+ * leaves): 9-13 us less GPU time at B = 4, Q = 21,504 in bf16, 21 us with softmax.
+ * The fork and join cost the calling thread about 45 us, so smaller calls, whose
+ * GPU time would not hide that, keep one stream.
  * Work before the call on `stream` happens before all of it, and work after the call
  * after all of it, so it stays stream-ordered and can be captured in a HIP graph.
  * The workspace holds 4 bytes per sample, then at least as many bytes as

@@ -535,9 +535,11 @@ def test_calls_replay_from_a_hip_graph(device, dtype, entry):
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
 
     lib = _lib.load()
-    # The workspace entry forks grad_sample onto its side stream from 2^19 samples:
-    # config 2 at full size (1 M samples) does; the plain entry takes a smaller call.
-    w = (make_workload(2) if entry == "workspace" else make_workload(2, batch=1, queries=2000)).to(device, dtype)
+    # The workspace entry forks grad_sample onto its side stream from 2^21 samples:
+    # config 2's pyramid over 5 images (2.6 M samples) does; the plain entry takes a
+    # smaller call.
+    w = (make_workload(2, batch=5) if entry == "workspace" else make_workload(2, batch=1, queries=2000))
+    w = w.to(device, dtype)
     value, shapes, starts, loc, attn = w.operands(softmax=True)
     B, S, H, D, Q, L, P = w.sizes
     codes = (_lib.DTYPE_CODES[value.dtype], _lib.DTYPE_CODES[loc.dtype], _lib.INDEX_CODES[shapes.dtype])
@@ -589,9 +591,9 @@ def test_concurrent_calls_from_two_threads_on_two_streams(device, entry):
     from deformops_amd.backends.hip import _lib  # noqa: PLC0415
 
     lib = _lib.load()
-    # Full config 2 (1 M samples) for the workspace entry, so that each thread forks
-    # onto a side stream of its own.
-    sizes = {} if entry == "workspace" else {"batch": 1, "queries": 1800}
+    # Config 2's pyramid over 5 images (2.6 M samples) for the workspace entry, so that
+    # each thread forks onto a side stream of its own.
+    sizes = {"batch": 5} if entry == "workspace" else {"batch": 1, "queries": 1800}
     works = [make_workload(2, seed=s, **sizes).to(device, dt) for s, dt in ((1, BF16), (2, F32))]
 
     def backward(w, stream):
